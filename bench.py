@@ -1,0 +1,416 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark: fused INT4 KV decode vs the same kernel on fp16 KV.
+
+``python bench.py [--steps K] [--warmup W] [--config C]`` prints one JSON line.
+
+* A step is one decode over the whole batch: the split-K partial kernel
+  plus the merge kernel.  For config 5 it also includes the quantize-on-append
+  of one new token per sequence.
+* Inputs are synthetic and built once, before timing.  Queries and K/V are
+  seeded N(0,1) fp16, with 1 % of (kv head, channel) pairs scaled x20 for
+  configs 2 and 3.  The caches are filled by this library's append kernel,
+  which is bit-exact with the CPU oracle.  Three copies of every cache are
+  rotated step by step, so the 256 MB MALL cannot serve a step from the
+  previous one.
+* ``value`` is whole-step HBM throughput: algorithmic bytes per step divided
+  by the step time.  Algorithmic bytes count each packed KV byte once, plus
+  the scales/zeros, q, out, block table and seq_lens.
+* ``roofline`` is for the dominant kernel, the decode partial.  Its achieved
+  bandwidth is its algorithmic bytes per launch divided by its average
+  duration, timed with HIP events on the stream it runs on.
+* ``cpu_baseline`` times the oracle's dequantise -> repeat_interleave -> SDPA
+  path (the reference's P1 pipeline) in torch on the host cores.  It runs on
+  a bounded sample (one sequence) and is scaled to the whole step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+# name, B, Hq, Hkv, D, context, kfmt, vfmt, kgs, vgs, paged, outliers, append
+CONFIGS = {
+    1: dict(name="gpt2-small B1 T1024 int4-asym-g32", B=1, Hq=12, Hkv=12, D=64, T=1024,
+            kfmt="int4_asym", vfmt="int4_asym", kgs=32, vgs=32, paged=False, outliers=0.0,
+            append=False),
+    2: dict(name="llama3-8b-gqa B8 T32768 int4-asym-g32 outliers1%x20", B=8, Hq=32, Hkv=8,
+            D=128, T=32768, kfmt="int4_asym", vfmt="int4_asym", kgs=32, vgs=32, paged=False,
+            outliers=0.01, append=False),
+    3: dict(name="llama3-8b-gqa paged B64 ctx~U[512,16384] pool2^18 int4-asym-g32", B=64,
+            Hq=32, Hkv=8, D=128, T=16384, kfmt="int4_asym", vfmt="int4_asym", kgs=32, vgs=32,
+            paged=True, outliers=0.01, append=False),
+    4: dict(name="long-context B1 T393216 int4-asym-g64", B=1, Hq=32, Hkv=8, D=128, T=393216,
+            kfmt="int4_asym", vfmt="int4_asym", kgs=64, vgs=64, paged=False, outliers=0.0,
+            append=False),
+    5: dict(name="qwen-gqa5 B16 T65536 K-int8-row V-int4-asym-g32 +append", B=16, Hq=40,
+            Hkv=8, D=128, T=65536, kfmt="int8", vfmt="int4_asym", kgs=128, vgs=32,
+            paged=False, outliers=0.0, append=True),
+}
+FMT = {"int4_sym": 0, "int4_asym": 1, "int8": 2, "fp16": 3}
+
+
+def per_token_head_bytes(fmt, d, gs):
+    if fmt == "fp16":
+        return 2 * d
+    if fmt == "int8":
+        return d + 2 * (d // gs)
+    return d // 2 + 2 * (d // gs) * (2 if fmt == "int4_asym" else 1)
+
+
+def algorithmic_bytes(cfg, seq_lens, kfmt, vfmt, bs):
+    tok = int(np.sum(seq_lens))
+    kv = tok * cfg["Hkv"] * (per_token_head_bytes(kfmt, cfg["D"], cfg["kgs"]) +
+                             per_token_head_bytes(vfmt, cfg["D"], cfg["vgs"]))
+    qo = 2 * cfg["B"] * cfg["Hq"] * cfg["D"] * 2
+    bt = int(np.sum([-(-int(n) // bs) for n in seq_lens])) * 4 + cfg["B"] * 4
+    return kv + qo + bt
+
+
+def make_seq_lens(cfg, seed):
+    """Decode lengths; with the append step each sequence holds T cached tokens
+    and decodes over T + 1 after the new token is written."""
+    if cfg["paged"]:
+        g = torch.Generator().manual_seed(seed)
+        return torch.randint(512, 16385, (cfg["B"],), generator=g).numpy().astype(np.int64)
+    return np.full(cfg["B"], cfg["T"] + (1 if cfg["append"] else 0), np.int64)
+
+
+def make_block_table(cfg, seq_lens, bs, seed):
+    width = -(-int(np.max(seq_lens)) // bs)
+    if cfg["paged"]:
+        pool = 1 << 18
+        g = torch.Generator().manual_seed(seed)
+        perm = torch.randperm(pool, generator=g).numpy().astype(np.int32)
+        bt = np.zeros((cfg["B"], width), np.int32)
+        cur = 0
+        for s, n in enumerate(seq_lens):
+            nb = -(-int(n) // bs)
+            bt[s, :nb] = perm[cur:cur + nb]
+            cur += nb
+        return bt, pool
+    bt = np.arange(cfg["B"] * width, dtype=np.int32).reshape(cfg["B"], width)
+    return bt, cfg["B"] * width
+
+
+def gen_rows(n, hkv, d, seed, outliers, dev, chunk=1 << 22):
+    """Seeded N(0,1) fp16 rows [n, hkv, d] generated on the host (bit-identical
+    for the oracle), outlier (head, channel) pairs scaled x20."""
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.ones(hkv * d)
+    if outliers > 0:
+        k = max(1, int(round(outliers * hkv * d)))
+        mask[torch.randperm(hkv * d, generator=g)[:k]] = 20.0
+    mask = mask.view(hkv, d)
+    out = torch.empty((n, hkv, d), dtype=torch.float16, device=dev)
+    rows = max(1, chunk // (hkv * d))
+    for i in range(0, n, rows):
+        m = min(rows, n - i)
+        x = torch.randn(m, hkv, d, generator=g) * mask
+        out[i:i + m] = x.to(torch.float16).to(dev)
+    return out
+
+
+class Caches:
+    """One set of paged cache planes on the device."""
+
+    def __init__(self, fmt, nb, bs, hkv, d, gs, dev):
+        self.fmt, self.gs = fmt, gs
+        if fmt == "fp16":
+            self.data = torch.zeros((nb, bs, hkv, d), dtype=torch.float16, device=dev)
+            self.scales = self.zeros = None
+            return
+        dt = torch.int8 if fmt == "int8" else torch.uint8
+        self.data = torch.zeros((nb, bs, hkv, d if fmt == "int8" else d // 2), dtype=dt,
+                                device=dev)
+        self.scales = torch.zeros((nb, bs, hkv, d // gs), dtype=torch.float16, device=dev)
+        self.zeros = torch.zeros_like(self.scales) if fmt == "int4_asym" else None
+
+    def clone(self):
+        c = Caches.__new__(Caches)
+        c.fmt, c.gs = self.fmt, self.gs
+        c.data = self.data.clone()
+        c.scales = None if self.scales is None else self.scales.clone()
+        c.zeros = None if self.zeros is None else self.zeros.clone()
+        return c
+
+    def plane(self):
+        from knlp_amd._lib import KvPlane
+        from knlp_amd.ops import _plane
+        return _plane(self.data, self.scales, self.zeros, FMT[self.fmt], self.gs)
+
+
+def fill(c: Caches, rows, slots, block_size):
+    import knlp_amd as K
+    if c.fmt == "fp16":
+        blk, off = slots // block_size, slots % block_size
+        c.data[blk, off] = rows
+    elif c.fmt == "int8":
+        K.reshape_and_cache_k_int8(rows, c.data, c.scales, slots, group_size=c.gs)
+    else:
+        K.reshape_and_cache_v_only_int4(rows, c.data, c.scales, slots, c.zeros,
+                                        asymmetric=c.fmt == "int4_asym", group_size=c.gs)
+
+
+def time_cpu_baseline(cfg, q_cpu, kc: Caches, vc: Caches, bt, seq_lens, bs):
+    """Oracle dequant -> repeat_interleave -> SDPA on the host, one sequence."""
+    sys.path.insert(0, ROOT)
+    from oracle import attention as A
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    s = int(np.argmax(seq_lens)) if cfg["paged"] else 0
+    n = int(seq_lens[s])
+    nblk = -(-n // bs)
+    blocks = torch.from_numpy(bt[s, :nblk].astype(np.int64)).to(kc.data.device)
+
+    def host_plane(c: Caches):
+        d = {"format": c.fmt, "group_size": c.gs, "data": c.data[blocks].cpu().numpy(),
+             "scales": None if c.scales is None else c.scales[blocks].cpu().numpy(),
+             "zeros": None if c.zeros is None else c.zeros[blocks].cpu().numpy()}
+        return d
+
+    kp, vp = host_plane(kc), host_plane(vc)
+    local_bt = np.arange(nblk, dtype=np.int32)[None]
+    q = q_cpu[s:s + 1].float().numpy()
+    times = []
+    out = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        out = A.decode_reference(q, kp, vp, local_bt, [n])
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    sample_bytes = algorithmic_bytes({**cfg, "B": 1}, [n], cfg["kfmt"], cfg["vfmt"], bs)
+    return {"value": round(sample_bytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"sequence {s} ({n} tokens, {cfg['Hq']}q/{cfg['Hkv']}kv heads) of the "
+                      f"workload; median of 3 runs of the oracle's dequant->SDPA in torch fp32",
+            "us_per_seq": round(t * 1e6, 1),
+            "us_per_step_equiv": round(t * 1e6 * float(np.sum(seq_lens)) / n, 1),
+            "cpu_model": _cpu_model()}, out, s
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, steps, partial_only=False,
+                     append=None):
+    """Launch `steps` decode steps rotating over cache copies; returns the
+    average ms per step measured with events on the current stream."""
+    import ctypes
+    from knlp_amd._lib import lib, check
+    from knlp_amd.ops import _stream
+    L = lib()
+    max_context = bt_d.shape[1] * bs
+    scale = 1.0 / (cfg["D"] ** 0.5)
+    planes = [(kc.plane(), vc.plane()) for kc, vc in copies]
+    stream = _stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        kp, vp = planes[i % len(planes)]
+        if append is not None:
+            append(i % len(planes))
+        if partial_only:
+            st = L.knlp_kv_decode_partial(
+                q.data_ptr(), 0, q.stride(0), q.stride(1), cfg["B"], cfg["Hq"], cfg["Hkv"],
+                cfg["D"], ctypes.byref(kp), ctypes.byref(vp), bt_d.data_ptr(), bt_d.stride(0),
+                sl_d.data_ptr(), bs, max_context, scale, split, ws.data_ptr(),
+                ws.numel() * 4, stream)
+        else:
+            st = L.knlp_kv_decode(
+                q.data_ptr(), 0, q.stride(0), q.stride(1), cfg["B"], cfg["Hq"], cfg["Hkv"],
+                cfg["D"], ctypes.byref(kp), ctypes.byref(vp), bt_d.data_ptr(), bt_d.stride(0),
+                sl_d.data_ptr(), bs, max_context, scale, split, ws.data_ptr(),
+                ws.numel() * 4, out.data_ptr(), 0, out.stride(0), out.stride(1), stream)
+        check(st, "decode")
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fp16", action="store_true")
+    ap.add_argument("--split-tokens", type=int, default=0)
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the decode path is single-GPU in this build "
+              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    sys.path.insert(0, ROOT)
+    import knlp_amd as K
+    from knlp_amd._lib import lib, check
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = CONFIGS[args.config]
+    c = args.config
+    bs = 16
+    B, Hq, Hkv, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["D"]
+    seq_lens = make_seq_lens(cfg, 5000 + c)
+    bt, nb = make_block_table(cfg, seq_lens, bs, 6000 + c)
+    L = lib()
+    max_context = bt.shape[1] * bs
+    split = args.split_tokens or L.knlp_kv_decode_split_tokens(B, Hkv, Hq, D, max_context)
+    print(f"# config {c}: {cfg['name']}; split_tokens={split}", file=sys.stderr, flush=True)
+
+    # ---- build inputs (untimed) -------------------------------------------------
+    g = torch.Generator().manual_seed(1000 + c)
+    q_cpu = torch.randn(B, Hq, D, generator=g).to(torch.float16)
+    q = q_cpu.to(dev)
+    bt_d = torch.from_numpy(bt).to(dev)
+    sl_d = torch.from_numpy(seq_lens.astype(np.int32)).to(dev)
+    fill_lens = seq_lens - 1 if cfg["append"] else seq_lens
+    slots = torch.cat([bt_d[s, (torch.arange(int(n), device=dev) // bs)].to(torch.int64) * bs
+                       + torch.arange(int(n), device=dev) % bs
+                       for s, n in enumerate(fill_lens)])
+    n_tok = slots.numel()
+    kc = Caches(cfg["kfmt"], nb, bs, Hkv, D, cfg["kgs"], dev)
+    vc = Caches(cfg["vfmt"], nb, bs, Hkv, D, cfg["vgs"], dev)
+    k16 = gen_rows(n_tok, Hkv, D, 2000 + c, cfg["outliers"], dev)
+    fill(kc, k16, slots, bs)
+    kf16 = None if args.no_fp16 else Caches("fp16", nb, bs, Hkv, D, D, dev)
+    if kf16 is not None:
+        fill(kf16, k16, slots, bs)
+    del k16
+    v16 = gen_rows(n_tok, Hkv, D, 3000 + c, cfg["outliers"], dev)
+    fill(vc, v16, slots, bs)
+    vf16 = None if args.no_fp16 else Caches("fp16", nb, bs, Hkv, D, D, dev)
+    if vf16 is not None:
+        fill(vf16, v16, slots, bs)
+    del v16
+    torch.cuda.synchronize()
+    copies = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(args.copies - 1)]
+    print(f"# inputs built: {n_tok} tokens", file=sys.stderr, flush=True)
+
+    ws_bytes = L.knlp_kv_decode_workspace_bytes(B, Hq, D, max_context, split)
+    ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
+    out = torch.empty_like(q)
+
+    append = None
+    if cfg["append"]:
+        # one new token per sequence per step, written at the next free slot
+        new_k = gen_rows(B, Hkv, D, 7000 + c, 0.0, dev)
+        new_v = gen_rows(B, Hkv, D, 8000 + c, 0.0, dev)
+        pos = torch.from_numpy(fill_lens).to(dev)
+        app_slots = bt_d[torch.arange(B, device=dev), pos // bs].to(torch.int64) * bs + pos % bs
+
+        def append(i):
+            kcc, vcc = copies[i]
+            K.reshape_and_cache_k_int8(new_k, kcc.data, kcc.scales, app_slots,
+                                       group_size=kcc.gs)
+            K.reshape_and_cache_v_only_int4(new_v, vcc.data, vcc.scales, app_slots, vcc.zeros,
+                                            asymmetric=True, group_size=vcc.gs)
+
+    # ---- INT4 decode: warmup, timed steps, dominant-kernel timing ----------------
+    run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.warmup,
+                     append=append)
+    ms_step = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.steps,
+                               append=append)
+    ms_partial = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.steps,
+                                  partial_only=True)
+    print(f"# int4 step {ms_step * 1e3:.1f} us, partial {ms_partial * 1e3:.1f} us",
+          file=sys.stderr, flush=True)
+    # final output of an un-rotated step for the parity spot check
+    run_decode_steps(copies[:1], q, bt_d, sl_d, cfg, bs, split, ws, out, 1)
+    out_int4 = out.float().cpu().numpy()
+
+    alg = algorithmic_bytes(cfg, seq_lens, cfg["kfmt"], cfg["vfmt"], bs)
+    kind = K.decode_kernel_kind(Hq, Hkv, D, FMT[cfg["kfmt"]], cfg["kgs"], FMT[cfg["vfmt"]],
+                                cfg["vgs"])
+
+    res16 = {}
+    if kf16 is not None:
+        fcopies = [(kf16, vf16)] + [(kf16.clone(), vf16.clone()) for _ in range(args.copies - 1)]
+        del copies
+        fcfg = {**cfg, "kfmt": "fp16", "vfmt": "fp16", "kgs": D, "vgs": D}
+        run_decode_steps(fcopies, q, bt_d, sl_d, fcfg, bs, split, ws, out, args.warmup)
+        ms16 = run_decode_steps(fcopies, q, bt_d, sl_d, fcfg, bs, split, ws, out, args.steps)
+        ms16p = run_decode_steps(fcopies, q, bt_d, sl_d, fcfg, bs, split, ws, out, args.steps,
+                                 partial_only=True)
+        alg16 = algorithmic_bytes(fcfg, seq_lens, "fp16", "fp16", bs)
+        res16 = {"fp16_us_per_step": round(ms16 * 1e3, 2),
+                 "fp16_partial_us": round(ms16p * 1e3, 2),
+                 "fp16_step_GBs": round(alg16 / (ms16 * 1e-3) / 1e9, 1),
+                 "fp16_partial_pct_of_peak": round(
+                     100 * alg16 / (ms16p * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
+                 "int4_speedup_vs_fp16": round(ms16 / ms_step, 3)}
+        print(f"# fp16 step {ms16 * 1e3:.1f} us", file=sys.stderr, flush=True)
+        del fcopies
+
+    cpu = None
+    parity = None
+    if not args.no_cpu_baseline and c != 4:
+        cpu, ref, s = time_cpu_baseline(cfg, q_cpu, kc, vc, bt, seq_lens, bs)
+        parity = float(np.nanmax(np.abs(out_int4[s] - ref[0])))
+        print(f"# cpu baseline {cpu['us_per_seq']:.0f} us/seq; parity max-abs {parity:.2e}",
+              file=sys.stderr, flush=True)
+
+    step_gbs = alg / (ms_step * 1e-3) / 1e9
+    part_gbs = alg / (ms_partial * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"decode_cfg{c}_traffic.json")
+    if os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    rec = {
+        "metric": "decode-attn us/step and achieved HBM GB/s (% of peak), INT4 vs fp16 KV",
+        "value": round(step_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "us_per_step": round(ms_step * 1e3, 2),
+        "pct_of_peak": round(100 * step_gbs / HBM_PEAK_GBS, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4-asym-g32 KV, fp16 q, fp32 accumulate" if c != 5 else
+                 "int8 K / int4-asym V, fp16 q, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) fp16, host-generated; caches filled by the "
+                "bit-exact append kernel)",
+        "config": {"workload": cfg["name"], "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+                   "head_dim": D, "context": int(np.max(seq_lens)),
+                   "total_tokens": int(np.sum(seq_lens)), "block_size": bs,
+                   "split_tokens": split, "cache_copies_rotated": args.copies,
+                   "decode_kernel": kind, "parallelism": "single GPU"},
+        "algorithmic_bytes_per_step": alg,
+        "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(part_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "decode partial (split-K)",
+                     "avg_launch_us": round(ms_partial * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "parity_max_abs_vs_oracle": parity,
+        **res16,
+    }
+    print(json.dumps(rec))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

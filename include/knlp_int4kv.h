@@ -1,0 +1,175 @@
+/*
+ * knlp_int4kv.h -- C ABI of the MI355X (gfx950) INT4/INT8 KV-cache
+ * quantize-on-append and split-K decode-attention library.
+ *
+ * Every entry point takes raw device pointers, element strides, sizes and a
+ * hipStream_t (passed as void*), launches onto that stream, allocates nothing
+ * and never synchronises, so the calls are safe inside HIP graph capture.
+ * Return value: KNLP_OK (0) or a negative KNLP_ERR_* status; nothing is
+ * launched when the status is negative.
+ *
+ * Cache layouts are the reference's (mcgrof/knlp,
+ * fused-quant/fused_int4.v0.1.0.py = "F"):
+ *   packed INT4 codes  uint8 [num_blocks, block_size, num_kv_heads, D/2]
+ *                      low nibble = element 2i, high nibble = 2i+1 (F:359)
+ *   INT8 codes         int8  [num_blocks, block_size, num_kv_heads, D]
+ *   fp16 cache         fp16  [num_blocks, block_size, num_kv_heads, D]
+ *   scales / zeros     fp16  [num_blocks, block_size, num_kv_heads, D/G]
+ *   slot = block * block_size + offset; slot < 0 is skipped (F:266-271).
+ */
+#ifndef KNLP_INT4KV_H
+#define KNLP_INT4KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KNLP_ABI_VERSION 1
+
+enum knlp_status {
+  KNLP_OK = 0,
+  KNLP_ERR_SHAPE = -1,      /* unsupported or inconsistent sizes */
+  KNLP_ERR_DTYPE = -2,      /* unsupported element type / format */
+  KNLP_ERR_ALIGN = -3,      /* pointer or stride alignment violated */
+  KNLP_ERR_WORKSPACE = -4,  /* workspace missing or too small */
+  KNLP_ERR_LAUNCH = -5,     /* the HIP launch itself failed */
+  KNLP_ERR_ARG = -6         /* null pointer or invalid scalar argument */
+};
+
+/* element types of query / key / value / output tensors and index arrays */
+enum knlp_dtype {
+  KNLP_DT_F16 = 0,
+  KNLP_DT_BF16 = 1,
+  KNLP_DT_I32 = 2,
+  KNLP_DT_I64 = 3
+};
+
+/* storage format of one cache plane (K or V) */
+enum knlp_kv_format {
+  KNLP_KV_INT4_SYM = 0,   /* codes (n-8)*scale, F:328-357 */
+  KNLP_KV_INT4_ASYM = 1,  /* codes n*scale + zero, F:308-327 */
+  KNLP_KV_INT8_SYM = 2,   /* int8 n*scale, F:1270-1284 */
+  KNLP_KV_FP16 = 3        /* plain fp16 cache, no scales */
+};
+
+/*
+ * One paged cache plane: codes plus per-group fp16 scale (and zero-point for
+ * KNLP_KV_INT4_ASYM).  Strides are in elements of the respective array
+ * (bytes for uint8/int8 codes, halves for fp16 arrays) over the
+ * (block, page-offset, head) axes; the last axis must be contiguous.
+ * The reference passes the same numbers as separate Triton kernel arguments
+ * (F:226-250, F:676-697).
+ */
+typedef struct knlp_kv_plane {
+  void* data;
+  void* scales;             /* NULL for KNLP_KV_FP16 */
+  void* zeros;              /* used only by KNLP_KV_INT4_ASYM */
+  int64_t stride_block, stride_page, stride_head;
+  int64_t s_stride_block, s_stride_page, s_stride_head;
+  int64_t z_stride_block, z_stride_page, z_stride_head;
+  int32_t format;           /* enum knlp_kv_format */
+  int32_t group_size;       /* elements per scale group along head_dim */
+} knlp_kv_plane;
+
+int knlp_abi_version(void);
+const char* knlp_status_string(int status);
+
+/*
+ * Quantize-on-append.  Replaces reshape_and_cache_int4 (F:418-472),
+ * reshape_and_cache_v_only_int4 (F:603-647, key == NULL),
+ * reshape_and_cache_k_int8 (F:1287-1312, key plane format INT8, value NULL)
+ * and reshape_and_cache_v_int8 (F:1619-1650, value plane format INT8).
+ * key / value: [num_tokens, num_heads, head_size] fp16 or bf16 (src_dtype),
+ * last axis contiguous.  clip_ratio is the symmetric INT4 trimmed-mean clip
+ * (F:70-72); 0 disables it.  slot_mapping: [num_tokens] int32 or int64.
+ */
+int knlp_kv_append(const void* key, const void* value, int32_t src_dtype,
+                   int64_t num_tokens, int32_t num_heads, int32_t head_size,
+                   int64_t key_stride_token, int64_t key_stride_head,
+                   int64_t value_stride_token, int64_t value_stride_head,
+                   const knlp_kv_plane* key_cache,
+                   const knlp_kv_plane* value_cache,
+                   const void* slot_mapping, int32_t slot_dtype,
+                   int32_t block_size, float clip_ratio, void* stream);
+
+/*
+ * Split-K plan: tokens per split for a batch whose longest possible context
+ * is max_context (= block-table width * block_size; no device read-back).
+ * Returns the split length in tokens (> 0) or a negative status.
+ */
+int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads,
+                                    int32_t num_q_heads, int32_t head_size,
+                                    int32_t max_context);
+
+/* Bytes of fp32 workspace decode needs for this shape and split length. */
+int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                       int32_t head_size, int32_t max_context,
+                                       int32_t split_tokens);
+
+/*
+ * Stage 2: split-K decode attention over paged caches.  Replaces the launch
+ * in fused_int4_decode (F:901-979), kint8_vint4_decode (F:1496-1554) and the
+ * other precision variants (F:1159-1225, F:1796-1848, F:1975-2028): the
+ * reference runs one program per (sequence, q head) over the whole context;
+ * here one wave per (sequence, kv head, split) serves all q heads of the GQA
+ * group and writes an unnormalised partial (acc, max, sum) per split into the
+ * caller's fp32 workspace.
+ * query: [num_seqs, num_q_heads, head_size] fp16/bf16; block_table int32
+ * [num_seqs, >= ceil(max_context / block_size)]; seq_lens int32 [num_seqs].
+ * softmax_scale multiplies q.k (the reference fixes it to 1/sqrt(head_size),
+ * F:924).
+ */
+int knlp_kv_decode_partial(const void* query, int32_t q_dtype,
+                           int64_t q_stride_seq, int64_t q_stride_head,
+                           int32_t num_seqs, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_size,
+                           const knlp_kv_plane* key_cache,
+                           const knlp_kv_plane* value_cache,
+                           const int32_t* block_table, int64_t bt_stride_seq,
+                           const int32_t* seq_lens, int32_t block_size,
+                           int32_t max_context, float softmax_scale,
+                           int32_t split_tokens, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+/*
+ * Stage 3: merge the per-split partial softmax states (log-sum-exp combine)
+ * and write the output [num_seqs, num_q_heads, head_size] in out_dtype
+ * (fp32 -> fp16 rounding, then bf16 when out_dtype is bf16, as F:891-894 and
+ * the reference's store into empty_like(query) do).  A sequence with
+ * seq_len == 0 yields NaN, as the reference's 0/0 does (F:886-887).
+ * No counterpart in the reference (it has no split-K).
+ */
+int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes,
+                         const int32_t* seq_lens, int32_t num_seqs,
+                         int32_t num_q_heads, int32_t head_size,
+                         int32_t max_context, int32_t split_tokens,
+                         void* out, int32_t out_dtype, int64_t o_stride_seq,
+                         int64_t o_stride_head, void* stream);
+
+/* knlp_kv_decode_partial followed by knlp_kv_decode_merge on one stream. */
+int knlp_kv_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                   int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                   int32_t num_kv_heads, int32_t head_size,
+                   const knlp_kv_plane* key_cache,
+                   const knlp_kv_plane* value_cache,
+                   const int32_t* block_table, int64_t bt_stride_seq,
+                   const int32_t* seq_lens, int32_t block_size,
+                   int32_t max_context, float softmax_scale,
+                   int32_t split_tokens, void* workspace,
+                   int64_t workspace_bytes, void* out, int32_t out_dtype,
+                   int64_t o_stride_seq, int64_t o_stride_head, void* stream);
+
+/* Which decode kernel a shape dispatches to: 1 = MFMA path, 0 = VALU path,
+ * negative = unsupported (status).  Lets tests and the bench report it. */
+int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t head_size, int32_t k_format,
+                               int32_t k_group_size, int32_t v_format,
+                               int32_t v_group_size, int32_t q_dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KNLP_INT4KV_H */

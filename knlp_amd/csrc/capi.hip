@@ -1,0 +1,273 @@
+// extern "C" entry points: argument validation, split planning, dispatch.
+// No allocation and no synchronisation happens here; every launch goes to
+// the caller's stream.
+#include <cmath>
+
+#include "kv_decode.h"
+
+namespace knlp {
+int launch_append(const void* key, const void* value, int src_bf16, int64_t num_tokens,
+                  int num_heads, int head_size, int64_t kst, int64_t ksh, int64_t vst,
+                  int64_t vsh, const knlp_kv_plane& KP, const knlp_kv_plane& VP,
+                  const void* slots, int slots64, int block_size, float clip_ratio,
+                  hipStream_t stream);
+}
+
+using namespace knlp;
+
+namespace {
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Validate one plane for a head size.  `need_row_align` is the byte alignment
+// each (block, page, head) row of codes must have for the vector loads used.
+int check_plane(const knlp_kv_plane* P, int head_size, bool decode) {
+  if (P == nullptr || P->data == nullptr) return KNLP_ERR_ARG;
+  const int f = P->format;
+  if (f < KNLP_KV_INT4_SYM || f > KNLP_KV_FP16) return KNLP_ERR_DTYPE;
+  if (f != KNLP_KV_FP16) {
+    const int gs = P->group_size;
+    if (P->scales == nullptr) return KNLP_ERR_ARG;
+    if (f == KNLP_KV_INT4_ASYM && P->zeros == nullptr) return KNLP_ERR_ARG;
+    if (!is_pow2(gs) || gs < 16 || gs > 128 || gs > head_size || head_size % gs != 0)
+      return KNLP_ERR_SHAPE;
+  }
+  // vector loads: decode reads 4 / 8 / 16 bytes per lane, append writes 1 / 2 / 4
+  const int64_t eb = f == KNLP_KV_FP16 ? 2 : 1;
+  const int64_t vec = decode ? (f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM ? 4 : (f == KNLP_KV_INT8_SYM ? 8 : 16))
+                             : (f == KNLP_KV_FP16 ? 4 : (f == KNLP_KV_INT8_SYM ? 2 : 1));
+  if (!aligned(P->data, vec)) return KNLP_ERR_ALIGN;
+  if ((P->stride_block * eb) % vec || (P->stride_page * eb) % vec || (P->stride_head * eb) % vec)
+    return KNLP_ERR_ALIGN;
+  if (f != KNLP_KV_FP16 && !aligned(P->scales, 2)) return KNLP_ERR_ALIGN;
+  return KNLP_OK;
+}
+
+int check_head_size(int head_size) {
+  return (head_size == 32 || head_size == 64 || head_size == 128 || head_size == 256)
+             ? KNLP_OK
+             : KNLP_ERR_SHAPE;
+}
+
+int num_cus() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n > 0)
+      cached = n;
+    else
+      cached = 256;   // MI355X
+  }
+  return cached;
+}
+
+int heads_per_block(int num_kv_heads) {
+  // all kv heads of a page in one workgroup (one wave each), up to 8 waves,
+  // so every 128-byte line a workgroup touches is consumed inside it
+  for (int h = 8; h >= 1; h >>= 1)
+    if (num_kv_heads % h == 0) return h;
+  return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int knlp_abi_version(void) { return KNLP_ABI_VERSION; }
+
+const char* knlp_status_string(int status) {
+  switch (status) {
+    case KNLP_OK: return "ok";
+    case KNLP_ERR_SHAPE: return "unsupported or inconsistent shape";
+    case KNLP_ERR_DTYPE: return "unsupported dtype or cache format";
+    case KNLP_ERR_ALIGN: return "pointer or stride misaligned for vector access";
+    case KNLP_ERR_WORKSPACE: return "workspace missing or too small";
+    case KNLP_ERR_LAUNCH: return "HIP kernel launch failed";
+    case KNLP_ERR_ARG: return "null pointer or invalid argument";
+    default: return "unknown status";
+  }
+}
+
+int knlp_kv_append(const void* key, const void* value, int32_t src_dtype, int64_t num_tokens,
+                   int32_t num_heads, int32_t head_size, int64_t key_stride_token,
+                   int64_t key_stride_head, int64_t value_stride_token,
+                   int64_t value_stride_head, const knlp_kv_plane* key_cache,
+                   const knlp_kv_plane* value_cache, const void* slot_mapping,
+                   int32_t slot_dtype, int32_t block_size, float clip_ratio, void* stream) {
+  if (key == nullptr && value == nullptr) return KNLP_ERR_ARG;
+  if (slot_mapping == nullptr) return KNLP_ERR_ARG;
+  if (src_dtype != KNLP_DT_F16 && src_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  if (slot_dtype != KNLP_DT_I32 && slot_dtype != KNLP_DT_I64) return KNLP_ERR_DTYPE;
+  if (num_tokens < 0 || num_heads <= 0 || block_size <= 0) return KNLP_ERR_SHAPE;
+  if (!(clip_ratio >= 0.0f) || std::isinf(clip_ratio)) return KNLP_ERR_ARG;
+  int st = check_head_size(head_size);
+  if (st) return st;
+  knlp_kv_plane kp{}, vp{};
+  if (key != nullptr) {
+    if ((st = check_plane(key_cache, head_size, false))) return st;
+    if (key_cache->format == KNLP_KV_FP16 && src_dtype != KNLP_DT_F16) return KNLP_ERR_DTYPE;
+    if (!aligned(key, 4) || key_stride_token % 2 || key_stride_head % 2) return KNLP_ERR_ALIGN;
+    kp = *key_cache;
+  }
+  if (value != nullptr) {
+    if ((st = check_plane(value_cache, head_size, false))) return st;
+    if (value_cache->format == KNLP_KV_FP16 && src_dtype != KNLP_DT_F16) return KNLP_ERR_DTYPE;
+    if (!aligned(value, 4) || value_stride_token % 2 || value_stride_head % 2)
+      return KNLP_ERR_ALIGN;
+    vp = *value_cache;
+  }
+  return launch_append(key, value, src_dtype == KNLP_DT_BF16, num_tokens, num_heads, head_size,
+                       key_stride_token, key_stride_head, value_stride_token,
+                       value_stride_head, kp, vp, slot_mapping, slot_dtype == KNLP_DT_I64,
+                       block_size, clip_ratio, static_cast<hipStream_t>(stream));
+}
+
+int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads, int32_t num_q_heads,
+                                    int32_t head_size, int32_t max_context) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || max_context <= 0 || head_size <= 0)
+    return KNLP_ERR_SHAPE;
+  (void)num_q_heads;
+  // Aim for about two resident workgroups per CU over the whole batch, but
+  // never below 256 tokens per split (partials cost (D+2)*4 bytes per q head
+  // per split on each side of the merge) and always a multiple of 64 tokens.
+  const int64_t groups = static_cast<int64_t>(num_seqs) *
+                         ((num_kv_heads + heads_per_block(num_kv_heads) - 1) /
+                          heads_per_block(num_kv_heads));
+  const int64_t target = 2LL * num_cus();
+  int64_t splits = (target + groups - 1) / groups;
+  if (splits < 1) splits = 1;
+  int64_t tok = (max_context + splits - 1) / splits;
+  if (tok < 256) tok = 256;
+  tok = (tok + 63) / 64 * 64;
+  if (tok > max_context) tok = (static_cast<int64_t>(max_context) + 63) / 64 * 64;
+  return static_cast<int32_t>(tok);
+}
+
+int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t head_size,
+                                       int32_t max_context, int32_t split_tokens) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || head_size <= 0 || max_context <= 0 ||
+      split_tokens <= 0)
+    return KNLP_ERR_SHAPE;
+  const int ns = (max_context + split_tokens - 1) / split_tokens;
+  return workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
+}
+
+int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_size,
+                               int32_t k_format, int32_t k_group_size, int32_t v_format,
+                               int32_t v_group_size, int32_t q_dtype) {
+  if (num_kv_heads <= 0 || num_q_heads % num_kv_heads) return KNLP_ERR_SHAPE;
+  const int g = num_q_heads / num_kv_heads;
+  if (g > 8) return KNLP_ERR_SHAPE;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
+  return mfma_supported(g, head_size, k_format, k_group_size, v_format, v_group_size,
+                        q_dtype == KNLP_DT_BF16)
+             ? 1
+             : 0;
+}
+
+int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                           int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_size,
+                           const knlp_kv_plane* key_cache, const knlp_kv_plane* value_cache,
+                           const int32_t* block_table, int64_t bt_stride_seq,
+                           const int32_t* seq_lens, int32_t block_size, int32_t max_context,
+                           float softmax_scale, int32_t split_tokens, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  if (query == nullptr || block_table == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
+  if (q_dtype != KNLP_DT_F16 && q_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
+      max_context <= 0 || split_tokens <= 0 || split_tokens % 64)
+    return KNLP_ERR_SHAPE;
+  if (num_q_heads % num_kv_heads) return KNLP_ERR_SHAPE;
+  const int kind = knlp_kv_decode_kernel_kind(num_q_heads, num_kv_heads, head_size,
+                                              key_cache ? key_cache->format : -1,
+                                              key_cache ? key_cache->group_size : 0,
+                                              value_cache ? value_cache->format : -1,
+                                              value_cache ? value_cache->group_size : 0,
+                                              q_dtype);
+  if (kind < 0) return kind;
+  int st;
+  if ((st = check_plane(key_cache, head_size, true))) return st;
+  if ((st = check_plane(value_cache, head_size, true))) return st;
+  if (!std::isfinite(softmax_scale)) return KNLP_ERR_ARG;
+  if (!aligned(query, 16) || q_stride_seq % 8 || q_stride_head % 8) return KNLP_ERR_ALIGN;
+  if (num_seqs == 0) return KNLP_OK;
+  const int ns = (max_context + split_tokens - 1) / split_tokens;
+  if (ns > 65535) return KNLP_ERR_SHAPE;
+  const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
+  if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16))
+    return KNLP_ERR_WORKSPACE;
+
+  DecodeArgs a{};
+  a.q = static_cast<const uint16_t*>(query);
+  a.q_stride_seq = q_stride_seq;
+  a.q_stride_head = q_stride_head;
+  a.q_bf16 = q_dtype == KNLP_DT_BF16;
+  a.num_seqs = num_seqs;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.kp = *key_cache;
+  a.vp = *value_cache;
+  a.block_table = block_table;
+  a.bt_stride = bt_stride_seq;
+  a.seq_lens = seq_lens;
+  a.block_size = block_size;
+  a.split_tokens = split_tokens;
+  a.num_splits = ns;
+  a.max_context = max_context;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (kind == 1) return launch_decode_mfma(a, head_size, s);
+  return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), s);
+}
+
+int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const int32_t* seq_lens,
+                         int32_t num_seqs, int32_t num_q_heads, int32_t head_size,
+                         int32_t max_context, int32_t split_tokens, void* out, int32_t out_dtype,
+                         int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
+  if (out == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
+  if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  if (num_seqs < 0 || num_q_heads <= 0 || max_context <= 0 || split_tokens <= 0)
+    return KNLP_ERR_SHAPE;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
+  if (!aligned(out, 2)) return KNLP_ERR_ALIGN;
+  if (num_seqs == 0) return KNLP_OK;
+  const int ns = (max_context + split_tokens - 1) / split_tokens;
+  const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
+  if (workspace == nullptr || workspace_bytes < need) return KNLP_ERR_WORKSPACE;
+  float *po, *pml;
+  workspace_views(const_cast<void*>(workspace), num_seqs, num_q_heads, head_size, ns, &po, &pml);
+  return launch_merge(po, pml, seq_lens, num_seqs, num_q_heads, head_size, max_context,
+                      split_tokens, ns, out,
+                      out_dtype == KNLP_DT_BF16, o_stride_seq, o_stride_head,
+                      static_cast<hipStream_t>(stream));
+}
+
+int knlp_kv_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                   int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                   int32_t num_kv_heads, int32_t head_size, const knlp_kv_plane* key_cache,
+                   const knlp_kv_plane* value_cache, const int32_t* block_table,
+                   int64_t bt_stride_seq, const int32_t* seq_lens, int32_t block_size,
+                   int32_t max_context, float softmax_scale, int32_t split_tokens,
+                   void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
+                   int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
+  if (out == nullptr) return KNLP_ERR_ARG;
+  if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  int st = knlp_kv_decode_partial(query, q_dtype, q_stride_seq, q_stride_head, num_seqs,
+                                  num_q_heads, num_kv_heads, head_size, key_cache, value_cache,
+                                  block_table, bt_stride_seq, seq_lens, block_size, max_context,
+                                  softmax_scale, split_tokens, workspace, workspace_bytes,
+                                  stream);
+  if (st) return st;
+  return knlp_kv_decode_merge(workspace, workspace_bytes, seq_lens, num_seqs, num_q_heads,
+                              head_size, max_context, split_tokens, out, out_dtype, o_stride_seq,
+                              o_stride_head, stream);
+}
+
+}  // extern "C"

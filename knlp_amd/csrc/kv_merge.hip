@@ -1,0 +1,112 @@
+// Stage 3: merge per-split partial softmax states (new; the reference has no
+// split-K).  For one (sequence, q head) with splits i = 0..n-1 holding
+// (o_i[D], m_i, l_i) -- unnormalised accumulator, running max in log2 units,
+// running sum -- the result is
+//     M = max m_i,  L = sum l_i 2^(m_i - M),  out = sum o_i 2^(m_i - M) / L,
+// rounded fp32 -> fp16 (F:891-894) and then to bf16 when the output tensor is
+// bf16.  n = ceil(seq_len / split_tokens); n = 0 gives 0/0 = NaN, matching the
+// reference's acc / l_i with l_i = 0 (F:886-887).
+//
+// One block of 4 waves per (sequence, q head): wave w folds splits
+// w, w+4, ... with an online (max-rescaling) combine, then the four wave
+// states are combined through LDS.
+#include "kv_decode.h"
+
+namespace knlp {
+
+template <int D>
+__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_o,
+                                                    const float* __restrict__ part_ml,
+                                                    const int32_t* __restrict__ seq_lens,
+                                                    int hq, int max_context,
+                                                    int split_tokens, int num_splits,
+                                                    void* __restrict__ out, int out_bf16,
+                                                    int64_t o_stride_seq, int64_t o_stride_head) {
+  constexpr int E = D >= kWave ? D / kWave : 1;     // elements per lane
+  constexpr int NW = 4;
+  __shared__ float s_o[NW][D];
+  __shared__ float s_m[NW], s_l[NW];
+  const int h = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int n_len = min(seq_lens[seq], max_context);
+  const int ns = min(num_splits, (n_len + split_tokens - 1) / split_tokens);
+  const int64_t row0 = (static_cast<int64_t>(seq) * hq + h) * num_splits;
+
+  float M = -INFINITY, L = 0.0f, o[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) o[e] = 0.0f;
+  const bool active = lane * E < D;
+  for (int i = w; i < ns; i += NW) {
+    const float mi = part_ml[2 * (row0 + i)];
+    const float li = part_ml[2 * (row0 + i) + 1];
+    const float mn = fmaxf(M, mi);
+    const float a_old = exp2f(M - mn);
+    const float a_new = exp2f(mi - mn);
+    L = L * a_old + li * a_new;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float oi = active ? part_o[(row0 + i) * D + lane * E + e] : 0.0f;
+      o[e] = o[e] * a_old + oi * a_new;
+    }
+    M = mn;
+  }
+  if (lane == 0) {
+    s_m[w] = M;
+    s_l[w] = L;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (active) s_o[w][lane * E + e] = o[e];
+  __syncthreads();
+  if (w != 0) return;
+  float Mg = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) Mg = fmaxf(Mg, s_m[k]);
+  float Lg = 0.0f, f[NW];
+#pragma unroll
+  for (int k = 0; k < NW; ++k) {
+    // a wave that saw no split has M = -inf and contributes nothing
+    f[k] = s_m[k] == -INFINITY ? 0.0f : exp2f(s_m[k] - Mg);
+    Lg += s_l[k] * f[k];
+  }
+  if (!active) return;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane * E + e;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) acc += s_o[k][d] * f[k];
+    const float r = acc / Lg;
+    const uint16_t hb = float_to_half_bits(r);
+    const uint16_t ob = out_bf16 ? float_to_bf16_bits(half_bits_to_float(hb)) : hb;
+    static_cast<uint16_t*>(out)[seq * o_stride_seq + h * o_stride_head + d] = ob;
+  }
+}
+
+int launch_merge(const float* part_o, const float* part_ml, const int32_t* seq_lens,
+                 int num_seqs, int hq, int head_size, int max_context, int split_tokens,
+                 int num_splits,
+                 void* out, int out_bf16, int64_t o_stride_seq, int64_t o_stride_head,
+                 hipStream_t stream) {
+  const dim3 grid(hq, num_seqs);
+  const dim3 block(256);
+  switch (head_size) {
+#define KNLP_MERGE_D(D)                                                                 \
+  case D:                                                                               \
+    hipLaunchKernelGGL(merge_kernel<D>, grid, block, 0, stream, part_o, part_ml,        \
+                       seq_lens, hq, max_context, split_tokens, num_splits, out, out_bf16,           \
+                       o_stride_seq, o_stride_head);                                    \
+    break;
+    KNLP_MERGE_D(64)
+    KNLP_MERGE_D(128)
+    KNLP_MERGE_D(256)
+#undef KNLP_MERGE_D
+    default:
+      return KNLP_ERR_SHAPE;
+  }
+  return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
+}
+
+}  // namespace knlp

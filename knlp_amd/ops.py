@@ -1,0 +1,279 @@
+"""Drop-in replacements for the module functions of knlp's fused INT4 backend.
+
+Same names, argument order, defaults and in-place / return conventions as
+``fused-quant/fused_int4.v0.1.0.py`` (F): the write functions mutate the
+caller's caches and return None; the decode functions return a new tensor
+shaped like ``query`` (``torch.empty_like(query)``, F:932).  Every function
+launches onto the current torch stream through the C ABI of
+``libknlp_int4kv.so`` and performs no host synchronisation, so the calls can
+be captured in a HIP graph.  There is no CPU fallback: a missing library
+raises.
+
+Extensions over the reference, all keyword-only and defaulting to the
+reference's behaviour:
+  * ``group_size`` / ``k_group_size`` / ``v_group_size`` -- the reference uses
+    the module-wide GROUP_SIZE for K and V alike (F:1412-1418); per-plane
+    sizes allow e.g. per-row INT8 K (group = head_size) with g32 INT4 V;
+  * ``clip_ratio`` -- defaults to OUTLIER_CLIP_RATIO like F:470;
+  * ``scale`` -- defaults to 1/sqrt(head_size) as F:924 fixes it;
+  * ``split_tokens`` -- split-K length, default from the library's plan.
+``block_n`` is accepted for signature compatibility and ignored: the HIP
+kernels pick their own token tiles.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import config
+from ._lib import (DT_BF16, DT_F16, DT_I32, DT_I64, KV_FP16, KV_INT4_ASYM, KV_INT4_SYM,
+                   KV_INT8_SYM, KvPlane, check, lib)
+
+GROUP_SIZE = config.GROUP_SIZE
+OUTLIER_CLIP_RATIO = config.OUTLIER_CLIP_RATIO
+ASYMMETRIC = config.ASYMMETRIC
+
+_SRC_DTYPES = {torch.float16: DT_F16, torch.bfloat16: DT_BF16}
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _require_cuda(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("knlp_amd ops need device tensors (the HIP path has no CPU fallback)")
+
+
+def _plane(cache: torch.Tensor, scales, zeros, fmt: int, group_size: int) -> KvPlane:
+    want = {KV_INT4_SYM: torch.uint8, KV_INT4_ASYM: torch.uint8, KV_INT8_SYM: torch.int8,
+            KV_FP16: torch.float16}[fmt]
+    if cache.dtype != want:
+        raise ValueError(f"cache dtype {cache.dtype} does not match format (want {want})")
+    if cache.dim() != 4 or cache.stride(3) != 1:
+        raise ValueError("cache must be [num_blocks, block_size, num_heads, packed_dim] "
+                         "with a contiguous last axis")
+    p = KvPlane()
+    p.data = cache.data_ptr()
+    p.stride_block, p.stride_page, p.stride_head = cache.stride()[:3]
+    p.format = fmt
+    p.group_size = group_size
+    if fmt != KV_FP16:
+        if scales is None or scales.dtype != torch.float16 or scales.dim() != 4 \
+                or scales.stride(3) != 1:
+            raise ValueError("scales must be fp16 [num_blocks, block_size, num_heads, num_groups]")
+        p.scales = scales.data_ptr()
+        p.s_stride_block, p.s_stride_page, p.s_stride_head = scales.stride()[:3]
+    if fmt == KV_INT4_ASYM:
+        if zeros is None or zeros.dtype != torch.float16 or zeros.stride(3) != 1:
+            raise ValueError("asymmetric mode needs fp16 zero-points shaped like the scales")
+        p.zeros = zeros.data_ptr()
+        p.z_stride_block, p.z_stride_page, p.z_stride_head = zeros.stride()[:3]
+    return p
+
+
+def _src_dtype(t: torch.Tensor) -> int:
+    if t.dtype not in _SRC_DTYPES:
+        raise ValueError(f"key/value dtype {t.dtype} not supported (fp16 or bf16)")
+    if t.dim() != 3 or t.stride(2) != 1:
+        raise ValueError("key/value must be [num_tokens, num_heads, head_size], last axis contiguous")
+    return _SRC_DTYPES[t.dtype]
+
+
+def _slot_dtype(slot_mapping: torch.Tensor) -> int:
+    if slot_mapping.dtype == torch.int64:
+        return DT_I64
+    if slot_mapping.dtype == torch.int32:
+        return DT_I32
+    raise ValueError("slot_mapping must be int32 or int64")
+
+
+def _append(key, value, kplane, vplane, slot_mapping, clip_ratio, block_size) -> None:
+    src = key if key is not None else value
+    dt = _src_dtype(src)
+    if key is not None and value is not None and key.dtype != value.dtype:
+        raise ValueError("key and value must share a dtype")
+    slot_mapping = slot_mapping.contiguous()
+    num_tokens, num_heads, head_size = src.shape
+    if slot_mapping.numel() < num_tokens:
+        raise ValueError("slot_mapping shorter than num_tokens")
+    st = lib().knlp_kv_append(
+        key.data_ptr() if key is not None else None,
+        value.data_ptr() if value is not None else None,
+        dt, num_tokens, num_heads, head_size,
+        key.stride(0) if key is not None else 0, key.stride(1) if key is not None else 0,
+        value.stride(0) if value is not None else 0, value.stride(1) if value is not None else 0,
+        ctypes.byref(kplane) if kplane is not None else None,
+        ctypes.byref(vplane) if vplane is not None else None,
+        slot_mapping.data_ptr(), _slot_dtype(slot_mapping),
+        int(block_size), float(clip_ratio), _stream())
+    check(st, "knlp_kv_append")
+
+
+def reshape_and_cache_int4(key, value, key_cache, value_cache, k_scales, v_scales,
+                           slot_mapping, k_zeros=None, v_zeros=None, asymmetric=False, *,
+                           group_size=None, clip_ratio=None) -> None:
+    """Quantise fp16/bf16 K and V to packed INT4 and write them at
+    ``slot_mapping`` into the paged caches (F:418-472).  Symmetric mode uses
+    the trimmed-mean outlier clip (F:328-357); asymmetric stores zero-points."""
+    _require_cuda(key, value, key_cache, value_cache, k_scales, v_scales, slot_mapping)
+    gs = group_size or GROUP_SIZE
+    fmt = KV_INT4_ASYM if asymmetric else KV_INT4_SYM
+    kp = _plane(key_cache, k_scales, k_zeros, fmt, gs)
+    vp = _plane(value_cache, v_scales, v_zeros, fmt, gs)
+    _append(key, value, kp, vp, slot_mapping,
+            OUTLIER_CLIP_RATIO if clip_ratio is None else clip_ratio, key_cache.shape[1])
+
+
+def reshape_and_cache_v_only_int4(value, value_cache, v_scales, slot_mapping, v_zeros=None,
+                                  asymmetric=False, *, group_size=None,
+                                  clip_ratio=None) -> None:
+    """V-only INT4 quantise-and-cache (F:603-647)."""
+    _require_cuda(value, value_cache, v_scales, slot_mapping)
+    gs = group_size or GROUP_SIZE
+    vp = _plane(value_cache, v_scales, v_zeros, KV_INT4_ASYM if asymmetric else KV_INT4_SYM, gs)
+    _append(None, value, None, vp, slot_mapping,
+            OUTLIER_CLIP_RATIO if clip_ratio is None else clip_ratio, value_cache.shape[1])
+
+
+def reshape_and_cache_k_int8(key, key_cache_int8, k_scales, slot_mapping, *,
+                             group_size=None) -> None:
+    """Symmetric INT8 K quantise-and-cache (F:1287-1312)."""
+    _require_cuda(key, key_cache_int8, k_scales, slot_mapping)
+    kp = _plane(key_cache_int8, k_scales, None, KV_INT8_SYM, group_size or GROUP_SIZE)
+    _append(key, None, kp, None, slot_mapping, 0.0, key_cache_int8.shape[1])
+
+
+def reshape_and_cache_v_int8(value, value_cache_int8, v_scales, slot_mapping, *,
+                             group_size=None) -> None:
+    """Symmetric INT8 V quantise-and-cache (F:1619-1650)."""
+    _require_cuda(value, value_cache_int8, v_scales, slot_mapping)
+    vp = _plane(value_cache_int8, v_scales, None, KV_INT8_SYM, group_size or GROUP_SIZE)
+    _append(None, value, None, vp, slot_mapping, 0.0, value_cache_int8.shape[1])
+
+
+def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, num_kv_heads,
+            head_size, scale=None, split_tokens=None) -> torch.Tensor:
+    _require_cuda(query, block_table, seq_lens)
+    if query.dtype not in _SRC_DTYPES:
+        raise ValueError(f"query dtype {query.dtype} not supported (fp16 or bf16)")
+    if query.dim() != 3 or query.stride(2) != 1 or query.shape[2] != head_size:
+        raise ValueError("query must be [num_seqs, num_heads, head_size], last axis contiguous")
+    num_seqs, num_heads, _ = query.shape
+    if num_heads % num_kv_heads:
+        raise ValueError("num_heads must be a multiple of num_kv_heads")
+    if block_table.dtype != torch.int32:
+        block_table = block_table.to(torch.int32)
+    if block_table.stride(1) != 1:
+        block_table = block_table.contiguous()
+    if seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous():
+        seq_lens = seq_lens.to(torch.int32).contiguous()
+    L = lib()
+    max_context = block_table.shape[1] * block_size
+    if split_tokens is None:
+        split_tokens = config.DECODE_SPLIT_TOKENS or L.knlp_kv_decode_split_tokens(
+            num_seqs, num_kv_heads, num_heads, head_size, max_context)
+        check(split_tokens, "knlp_kv_decode_split_tokens")
+    ws_bytes = L.knlp_kv_decode_workspace_bytes(max(num_seqs, 1), num_heads, head_size,
+                                                max_context, split_tokens)
+    check(ws_bytes, "knlp_kv_decode_workspace_bytes")
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=query.device)
+    out = torch.empty_like(query)
+    if scale is None:
+        scale = 1.0 / (head_size ** 0.5)                  # F:924
+    dt = _SRC_DTYPES[query.dtype]
+    st = L.knlp_kv_decode(
+        query.data_ptr(), dt, query.stride(0), query.stride(1), num_seqs, num_heads,
+        num_kv_heads, head_size, ctypes.byref(kp), ctypes.byref(vp),
+        block_table.data_ptr(), block_table.stride(0), seq_lens.data_ptr(), block_size,
+        max_context, float(scale), int(split_tokens), ws.data_ptr(), ws_bytes,
+        out.data_ptr(), dt, out.stride(0), out.stride(1), _stream())
+    check(st, "knlp_kv_decode")
+    return out
+
+
+def fused_int4_decode(query, key_cache, value_cache, k_scales, v_scales, block_table, seq_lens,
+                      num_kv_heads, head_size, block_n=64, k_zeros=None, v_zeros=None,
+                      asymmetric=False, *, group_size=None, scale=None,
+                      split_tokens=None) -> torch.Tensor:
+    """Decode attention over packed INT4 K and V (F:901-979)."""
+    _require_cuda(key_cache, value_cache, k_scales, v_scales)
+    gs = group_size or GROUP_SIZE
+    fmt = KV_INT4_ASYM if asymmetric else KV_INT4_SYM
+    kp = _plane(key_cache, k_scales, k_zeros, fmt, gs)
+    vp = _plane(value_cache, v_scales, v_zeros, fmt, gs)
+    return _decode(query, kp, vp, key_cache.shape[1], block_table, seq_lens, num_kv_heads,
+                   head_size, scale, split_tokens)
+
+
+def kint8_vint4_decode(query, key_cache_int8, value_cache_int4, k_scales, v_scales, block_table,
+                       seq_lens, num_kv_heads, head_size, block_n=64, v_zeros=None,
+                       asymmetric=False, *, k_group_size=None, v_group_size=None, scale=None,
+                       split_tokens=None) -> torch.Tensor:
+    """Decode with symmetric INT8 K and INT4 V (F:1496-1554)."""
+    _require_cuda(key_cache_int8, value_cache_int4, k_scales, v_scales)
+    kp = _plane(key_cache_int8, k_scales, None, KV_INT8_SYM, k_group_size or GROUP_SIZE)
+    vp = _plane(value_cache_int4, v_scales, v_zeros,
+                KV_INT4_ASYM if asymmetric else KV_INT4_SYM, v_group_size or GROUP_SIZE)
+    return _decode(query, kp, vp, key_cache_int8.shape[1], block_table, seq_lens, num_kv_heads,
+                   head_size, scale, split_tokens)
+
+
+def kfp16_vint4_decode(query, key_cache_fp16, value_cache_int4, v_scales, block_table, seq_lens,
+                       num_kv_heads, head_size, block_n=64, v_zeros=None, asymmetric=False, *,
+                       v_group_size=None, scale=None, split_tokens=None) -> torch.Tensor:
+    """Decode with fp16 K and INT4 V (F:1159-1225)."""
+    _require_cuda(key_cache_fp16, value_cache_int4, v_scales)
+    kp = _plane(key_cache_fp16, None, None, KV_FP16, head_size)
+    vp = _plane(value_cache_int4, v_scales, v_zeros,
+                KV_INT4_ASYM if asymmetric else KV_INT4_SYM, v_group_size or GROUP_SIZE)
+    return _decode(query, kp, vp, key_cache_fp16.shape[1], block_table, seq_lens, num_kv_heads,
+                   head_size, scale, split_tokens)
+
+
+def kint8_vint8_decode(query, key_cache_int8, value_cache_int8, k_scales, v_scales, block_table,
+                       seq_lens, num_kv_heads, head_size, block_n=64, *, k_group_size=None,
+                       v_group_size=None, scale=None, split_tokens=None) -> torch.Tensor:
+    """Decode with symmetric INT8 K and V (F:1796-1848)."""
+    _require_cuda(key_cache_int8, value_cache_int8, k_scales, v_scales)
+    kp = _plane(key_cache_int8, k_scales, None, KV_INT8_SYM, k_group_size or GROUP_SIZE)
+    vp = _plane(value_cache_int8, v_scales, None, KV_INT8_SYM, v_group_size or GROUP_SIZE)
+    return _decode(query, kp, vp, key_cache_int8.shape[1], block_table, seq_lens, num_kv_heads,
+                   head_size, scale, split_tokens)
+
+
+def kfp16_vint8_decode(query, key_cache_fp16, value_cache_int8, v_scales, block_table, seq_lens,
+                       num_kv_heads, head_size, block_n=64, *, v_group_size=None, scale=None,
+                       split_tokens=None) -> torch.Tensor:
+    """Decode with fp16 K and symmetric INT8 V (F:1975-2028)."""
+    _require_cuda(key_cache_fp16, value_cache_int8, v_scales)
+    kp = _plane(key_cache_fp16, None, None, KV_FP16, head_size)
+    vp = _plane(value_cache_int8, v_scales, None, KV_INT8_SYM, v_group_size or GROUP_SIZE)
+    return _decode(query, kp, vp, key_cache_fp16.shape[1], block_table, seq_lens, num_kv_heads,
+                   head_size, scale, split_tokens)
+
+
+def fp16_paged_decode(query, key_cache_fp16, value_cache_fp16, block_table, seq_lens,
+                      num_kv_heads, head_size, *, scale=None, split_tokens=None) -> torch.Tensor:
+    """The same split-K decode reading plain fp16 paged K and V caches.
+
+    Not a reference function: it is the fp16-KV instantiation of this
+    library's kernel used for the INT4-vs-fp16 comparison (the reference
+    compares against SDPA, scripts/spev01/tier5_fused_decode.py:341-348)."""
+    _require_cuda(key_cache_fp16, value_cache_fp16)
+    kp = _plane(key_cache_fp16, None, None, KV_FP16, head_size)
+    vp = _plane(value_cache_fp16, None, None, KV_FP16, head_size)
+    return _decode(query, kp, vp, key_cache_fp16.shape[1], block_table, seq_lens, num_kv_heads,
+                   head_size, scale, split_tokens)
+
+
+def decode_kernel_kind(num_heads, num_kv_heads, head_size, k_format, k_group_size, v_format,
+                       v_group_size, query_dtype=torch.float16) -> str:
+    """'mfma' or 'valu': which decode kernel the library dispatches a shape to."""
+    r = lib().knlp_kv_decode_kernel_kind(num_heads, num_kv_heads, head_size, k_format,
+                                         k_group_size, v_format, v_group_size,
+                                         _SRC_DTYPES[query_dtype])
+    check(r, "knlp_kv_decode_kernel_kind")
+    return "mfma" if r == 1 else "valu"

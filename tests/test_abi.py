@@ -1,0 +1,114 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, and rejects bad arguments before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from knlp_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "knlp_int4kv.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(knlp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    declared = _declared_functions()
+    assert declared, "header parse found nothing"
+    assert set(declared) == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+def test_abi_version_and_status_strings():
+    L = _lib.lib()
+    assert L.knlp_abi_version() == _lib.ABI_VERSION
+    for st in (0, -1, -2, -3, -4, -5, -6):
+        assert L.knlp_status_string(st)
+    assert L.knlp_status_string(-99) == b"unknown status"
+
+
+def test_split_plan_and_workspace():
+    L = _lib.lib()
+    st = L.knlp_kv_decode_split_tokens(8, 8, 32, 128, 32768)
+    assert st > 0 and st % 64 == 0
+    assert L.knlp_kv_decode_split_tokens(0, 8, 32, 128, 32768) == _lib.ERR_SHAPE
+    ws = L.knlp_kv_decode_workspace_bytes(8, 32, 128, 32768, st)
+    ns = -(-32768 // st)
+    assert ws == 8 * 32 * ns * (128 + 2) * 4
+
+
+def test_kernel_kind_rejects_bad_shapes():
+    L = _lib.lib()
+    assert L.knlp_kv_decode_kernel_kind(32, 7, 128, 1, 32, 1, 32, 0) == _lib.ERR_SHAPE
+    assert L.knlp_kv_decode_kernel_kind(32, 8, 96, 1, 32, 1, 32, 0) == _lib.ERR_SHAPE
+    assert L.knlp_kv_decode_kernel_kind(32, 8, 128, 1, 32, 1, 32, 0) in (0, 1)
+
+
+def _plane(fmt=_lib.KV_INT4_ASYM, gs=32, data=0x1000, scales=0x2000, zeros=0x3000):
+    p = _lib.KvPlane()
+    p.data, p.scales, p.zeros = data, scales, zeros
+    p.stride_block, p.stride_page, p.stride_head = 16 * 8 * 64, 8 * 64, 64
+    p.s_stride_block, p.s_stride_page, p.s_stride_head = 16 * 8 * 4, 8 * 4, 4
+    p.z_stride_block, p.z_stride_page, p.z_stride_head = 16 * 8 * 4, 8 * 4, 4
+    p.format, p.group_size = fmt, gs
+    return p
+
+
+def test_append_argument_validation_returns_before_launch():
+    L = _lib.lib()
+    kp, vp = _plane(), _plane()
+    args = dict(key=0x10000, value=0x20000, src=_lib.DT_F16, nt=4, nh=8, d=128)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return L.knlp_kv_append(a["key"], a["value"], a["src"], a["nt"], a["nh"], a["d"],
+                                1024, 128, 1024, 128, ctypes.byref(kw.get("kp", kp)),
+                                ctypes.byref(kw.get("vp", vp)), a.get("slots", 0x40000),
+                                kw.get("sd", _lib.DT_I64), 16, kw.get("clip", 10.0), None)
+
+    assert call(key=None, value=None) == _lib.ERR_ARG
+    assert call(slots=None) == _lib.ERR_ARG
+    assert call(src=_lib.DT_I32) == _lib.ERR_DTYPE
+    assert call(sd=_lib.DT_F16) == _lib.ERR_DTYPE
+    assert call(d=96) == _lib.ERR_SHAPE
+    assert call(clip=-1.0) == _lib.ERR_ARG
+    assert call(kp=_plane(gs=48)) == _lib.ERR_SHAPE
+    assert call(kp=_plane(zeros=None)) == _lib.ERR_ARG
+    assert call(kp=_plane(fmt=9)) == _lib.ERR_DTYPE
+
+
+def test_decode_argument_validation_returns_before_launch():
+    L = _lib.lib()
+    kp, vp = _plane(), _plane()
+
+    def call(ws=0x100000, ws_bytes=1 << 40, split=256, q=0x10000, d=128, hkv=8):
+        return L.knlp_kv_decode(q, _lib.DT_F16, 32 * 128, 128, 8, 32, hkv, d,
+                                ctypes.byref(kp), ctypes.byref(vp), 0x50000, 2048, 0x60000,
+                                16, 32768, 0.088, split, ws, ws_bytes, 0x70000, _lib.DT_F16,
+                                32 * 128, 128, None)
+
+    assert call(q=None) == _lib.ERR_ARG
+    assert call(split=100) == _lib.ERR_SHAPE
+    assert call(hkv=7) == _lib.ERR_SHAPE
+    assert call(ws=None) == _lib.ERR_WORKSPACE
+    assert call(ws_bytes=16) == _lib.ERR_WORKSPACE
+    assert call(q=0x10002) == _lib.ERR_ALIGN
+
+
+def test_ops_require_device_tensors():
+    import torch
+    from knlp_amd import ops
+    q = torch.zeros(1, 4, 64, dtype=torch.float16)
+    kc = torch.zeros(2, 16, 1, 32, dtype=torch.uint8)
+    sc = torch.zeros(2, 16, 1, 2, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        ops.fused_int4_decode(q, kc, kc, sc, sc, torch.zeros(1, 2, dtype=torch.int32),
+                              torch.ones(1, dtype=torch.int32), 1, 64)

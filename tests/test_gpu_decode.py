@@ -1,0 +1,190 @@
+"""GPU parity of split-K decode attention against the oracle's
+dequantise-then-SDPA path (scripts/v35_h100_bench.py:376-387; F:656-979,
+F:1318-1554 and the precision variants).
+
+Tolerance: max |gpu - oracle| <= 2e-3 + 2^-10 |oracle|, where the oracle is
+the fp32 result before output rounding; the relative term is the fp16
+output rounding (half an ulp) that both paths apply independently.
+"""
+import numpy as np
+import pytest
+import torch
+
+import knlp_amd as K
+from knlp_amd import _lib
+from oracle import attention as A
+from tests import kvgen
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ATOL = 2e-3
+RTOL = 2.0 ** -10
+
+
+def _build(seq_lens, hq, hkv, d, kfmt, vfmt, kgs, vgs, seed, bs=16, pool=None,
+           outliers=0.01, clip=10.0):
+    nb = pool or max(sum(-(-int(n) // bs) for n in seq_lens), 1) + 3
+    bt = kvgen.paged_table(seq_lens, bs, nb, 6000 + seed)
+    slots = kvgen.token_slots(bt, seq_lens, bs)
+    nt = len(slots)
+    k = kvgen.randn((nt, hkv, d), 2000 + seed, torch.float16, outliers).float().numpy()
+    v = kvgen.randn((nt, hkv, d), 3000 + seed, torch.float16, outliers).float().numpy()
+    kp = kvgen.empty_plane(kfmt, nb, bs, hkv, d, kgs)
+    vp = kvgen.empty_plane(vfmt, nb, bs, hkv, d, vgs)
+    if nt:
+        kvgen.fill_plane(kp, k, slots, clip)
+        kvgen.fill_plane(vp, v, slots, clip)
+    return bt, kp, vp
+
+
+def _query(nseq, hq, d, seed, dtype=torch.float16):
+    return kvgen.randn((nseq, hq, d), 1000 + seed, dtype)
+
+
+def _run(query, kp, vp, bt, seq_lens, hkv, d, split_tokens=None):
+    kd, ks, kz = kvgen.plane_to_torch(kp, DEV)
+    vd, vs, vz = kvgen.plane_to_torch(vp, DEV)
+    q = query.to(DEV)
+    btd = torch.from_numpy(bt).to(DEV)
+    sl = torch.tensor(seq_lens, dtype=torch.int32, device=DEV)
+    kf, vf = kp["format"], vp["format"]
+    kw = dict(split_tokens=split_tokens)
+    if kf.startswith("int4") and vf.startswith("int4"):
+        out = K.fused_int4_decode(q, kd, vd, ks, vs, btd, sl, hkv, d, k_zeros=kz, v_zeros=vz,
+                                  asymmetric=kf == "int4_asym", group_size=kp["group_size"], **kw)
+    elif kf == "int8" and vf.startswith("int4"):
+        out = K.kint8_vint4_decode(q, kd, vd, ks, vs, btd, sl, hkv, d, v_zeros=vz,
+                                   asymmetric=vf == "int4_asym", k_group_size=kp["group_size"],
+                                   v_group_size=vp["group_size"], **kw)
+    elif kf == "fp16" and vf.startswith("int4"):
+        out = K.kfp16_vint4_decode(q, kd, vd, vs, btd, sl, hkv, d, v_zeros=vz,
+                                   asymmetric=vf == "int4_asym", v_group_size=vp["group_size"],
+                                   **kw)
+    elif kf == "int8" and vf == "int8":
+        out = K.kint8_vint8_decode(q, kd, vd, ks, vs, btd, sl, hkv, d,
+                                   k_group_size=kp["group_size"], v_group_size=vp["group_size"],
+                                   **kw)
+    elif kf == "fp16" and vf == "int8":
+        out = K.kfp16_vint8_decode(q, kd, vd, vs, btd, sl, hkv, d,
+                                   v_group_size=vp["group_size"], **kw)
+    else:
+        out = K.fp16_paged_decode(q, kd, vd, btd, sl, hkv, d, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def _check(out, query, kp, vp, bt, seq_lens):
+    ref = A.decode_reference(query.float().numpy(), kp, vp, bt, seq_lens, round_output=False)
+    got = out.float().cpu().numpy()
+    valid = np.array([n > 0 for n in seq_lens])
+    err = np.abs(got[valid] - ref[valid])
+    bound = ATOL + RTOL * np.abs(ref[valid])
+    assert np.isfinite(got[valid]).all()
+    assert (err <= bound).all(), f"max abs err {err.max():.3e}"
+    if (~valid).any():
+        assert np.isnan(got[~valid]).all()       # 0/0 like the reference
+    return float(err.max()) if err.size else 0.0
+
+
+CASES = [
+    # name, seq_lens, hq, hkv, d, kfmt, vfmt, kgs, vgs
+    ("cfg1_gpt2_small", [1024], 12, 12, 64, 1, 1, 32, 32),
+    ("llama_gqa_asym", [3000, 777], 32, 8, 128, 1, 1, 32, 32),
+    ("llama_gqa_sym_clip", [1, 17, 511, 2049], 32, 8, 128, 0, 0, 32, 32),
+    ("g64_long", [5000], 32, 8, 128, 1, 1, 64, 64),
+    ("kint8_row_vint4_g5", [1500, 64], 40, 8, 128, 2, 1, 128, 32),
+    ("kint8_vint4_g32", [900], 32, 8, 128, 2, 1, 32, 32),
+    ("kfp16_vint4", [1200], 32, 8, 128, 3, 1, 128, 32),
+    ("kint8_vint8", [700], 32, 8, 128, 2, 2, 32, 32),
+    ("kfp16_vint8", [650], 32, 8, 128, 3, 2, 128, 32),
+    ("fp16_fp16", [2100, 33], 32, 8, 128, 3, 3, 128, 128),
+    ("d256_g8", [600], 64, 8, 256, 1, 1, 32, 32),
+    ("mha_d128", [300], 8, 8, 128, 0, 1, 32, 32),
+    ("g2_d64", [1000], 8, 4, 64, 1, 0, 32, 32),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_decode_matches_oracle(case):
+    name, seq_lens, hq, hkv, d, kf, vf, kgs, vgs = case
+    seed = abs(hash(name)) % 1000
+    bt, kp, vp = _build(seq_lens, hq, hkv, d, kf, vf, kgs, vgs, seed)
+    q = _query(len(seq_lens), hq, d, seed)
+    out = _run(q, kp, vp, bt, seq_lens, hkv, d)
+    _check(out, q, kp, vp, bt, seq_lens)
+
+
+def test_bf16_query_output_rounding():
+    seq_lens = [1300, 5]
+    bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, 21)
+    q = _query(2, 32, 128, 21, torch.bfloat16)
+    out = _run(q, kp, vp, bt, seq_lens, 8, 128)
+    assert out.dtype == torch.bfloat16
+    ref = A.decode_reference(q.float().numpy(), kp, vp, bt, seq_lens, round_output=False)
+    err = np.abs(out.float().cpu().numpy() - ref)
+    assert (err <= ATOL + 2.0 ** -7 * np.abs(ref)).all()
+
+
+def test_edge_lengths_zero_one_and_boundaries():
+    seq_lens = [0, 1, 63, 64, 65, 255, 256, 257]
+    bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, 31)
+    q = _query(len(seq_lens), 32, 128, 31)
+    out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=64)
+    _check(out, q, kp, vp, bt, seq_lens)
+    # context length 1 -> output is dequant(V_0) rounded to fp16
+    v0 = A.gather_sequence(A.dequant_plane(vp), bt[1], 1)[0]
+    want = np.repeat(v0, 4, axis=0).astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(out[1].float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("split", [64, 128, 512, 4096])
+def test_split_count_invariance(split):
+    seq_lens = [4000, 1000, 2500]
+    bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, 41)
+    q = _query(3, 32, 128, 41)
+    out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=split)
+    _check(out, q, kp, vp, bt, seq_lens)
+
+
+def test_block_table_permutation_invariance():
+    seq_lens = [2000]
+    bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, 51)
+    q = _query(1, 32, 128, 51)
+    a = _run(q, kp, vp, bt, seq_lens, 8, 128)
+    nb = kp["data"].shape[0]
+    perm = np.random.default_rng(5).permutation(nb)
+    inv = np.argsort(perm)
+    kp2 = {**kp, **{f: kp[f][inv] for f in ("data", "scales", "zeros")}}
+    vp2 = {**vp, **{f: vp[f][inv] for f in ("data", "scales", "zeros")}}
+    b = _run(q, kp2, vp2, perm[bt].astype(np.int32), seq_lens, 8, 128)
+    torch.testing.assert_close(a, b, atol=0, rtol=0)
+
+
+def test_gqa_heads_equal_per_head_runs():
+    """A q-group computed together equals each head computed alone (MHA)."""
+    seq_lens = [800]
+    hq, hkv, d = 32, 8, 128
+    bt, kp, vp = _build(seq_lens, hq, hkv, d, 1, 1, 32, 32, 61)
+    q = _query(1, hq, d, 61)
+    out = _run(q, kp, vp, bt, seq_lens, hkv, d)
+    # expand KV to one kv head per q head and rerun as MHA
+    rep = hq // hkv
+    kp2 = {**kp, **{f: np.repeat(kp[f], rep, axis=2) for f in ("data", "scales", "zeros")}}
+    vp2 = {**vp, **{f: np.repeat(vp[f], rep, axis=2) for f in ("data", "scales", "zeros")}}
+    out2 = _run(q, kp2, vp2, bt, seq_lens, hq, d)
+    err = (out.float() - out2.float()).abs().max().item()
+    assert err <= 2e-3
+
+
+def test_deterministic_repeat():
+    seq_lens = [3333, 1234]
+    bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, 71)
+    q = _query(2, 32, 128, 71)
+    a = _run(q, kp, vp, bt, seq_lens, 8, 128)
+    b = _run(q, kp, vp, bt, seq_lens, 8, 128)
+    torch.testing.assert_close(a, b, atol=0, rtol=0)
+
+
+def test_kernel_kind_reported():
+    kind = K.decode_kernel_kind(32, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32)
+    assert kind in ("mfma", "valu")
