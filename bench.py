@@ -254,11 +254,22 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp16", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES bytes 5 times (calibrates "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode path is single-GPU in this build "
               "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4, "launches": 5}))
+        return 0
 
     sys.path.insert(0, ROOT)
     import knlp_amd as K

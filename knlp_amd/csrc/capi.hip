@@ -98,11 +98,12 @@ int knlp_kv_append(const void* key, const void* value, int32_t src_dtype, int64_
                    int64_t value_stride_head, const knlp_kv_plane* key_cache,
                    const knlp_kv_plane* value_cache, const void* slot_mapping,
                    int32_t slot_dtype, int32_t block_size, float clip_ratio, void* stream) {
-  if (key == nullptr && value == nullptr) return KNLP_ERR_ARG;
-  if (slot_mapping == nullptr) return KNLP_ERR_ARG;
   if (src_dtype != KNLP_DT_F16 && src_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
   if (slot_dtype != KNLP_DT_I32 && slot_dtype != KNLP_DT_I64) return KNLP_ERR_DTYPE;
   if (num_tokens < 0 || num_heads <= 0 || block_size <= 0) return KNLP_ERR_SHAPE;
+  if (num_tokens == 0) return KNLP_OK;   // empty tensors may carry null data pointers
+  if (key == nullptr && value == nullptr) return KNLP_ERR_ARG;
+  if (slot_mapping == nullptr) return KNLP_ERR_ARG;
   if (!(clip_ratio >= 0.0f) || std::isinf(clip_ratio)) return KNLP_ERR_ARG;
   int st = check_head_size(head_size);
   if (st) return st;
@@ -177,11 +178,12 @@ int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_
                            const int32_t* seq_lens, int32_t block_size, int32_t max_context,
                            float softmax_scale, int32_t split_tokens, void* workspace,
                            int64_t workspace_bytes, void* stream) {
-  if (query == nullptr || block_table == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
   if (q_dtype != KNLP_DT_F16 && q_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
   if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
       max_context <= 0 || split_tokens <= 0 || split_tokens % 64)
     return KNLP_ERR_SHAPE;
+  if (num_seqs == 0) return KNLP_OK;   // empty tensors may carry null data pointers
+  if (query == nullptr || block_table == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
   if (num_q_heads % num_kv_heads) return KNLP_ERR_SHAPE;
   const int kind = knlp_kv_decode_kernel_kind(num_q_heads, num_kv_heads, head_size,
                                               key_cache ? key_cache->format : -1,
@@ -195,7 +197,6 @@ int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_
   if ((st = check_plane(value_cache, head_size, true))) return st;
   if (!std::isfinite(softmax_scale)) return KNLP_ERR_ARG;
   if (!aligned(query, 16) || q_stride_seq % 8 || q_stride_head % 8) return KNLP_ERR_ALIGN;
-  if (num_seqs == 0) return KNLP_OK;
   const int ns = (max_context + split_tokens - 1) / split_tokens;
   if (ns > 65535) return KNLP_ERR_SHAPE;
   const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
@@ -231,13 +232,13 @@ int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const i
                          int32_t num_seqs, int32_t num_q_heads, int32_t head_size,
                          int32_t max_context, int32_t split_tokens, void* out, int32_t out_dtype,
                          int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
-  if (out == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
   if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
   if (num_seqs < 0 || num_q_heads <= 0 || max_context <= 0 || split_tokens <= 0)
     return KNLP_ERR_SHAPE;
   if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
-  if (!aligned(out, 2)) return KNLP_ERR_ALIGN;
   if (num_seqs == 0) return KNLP_OK;
+  if (out == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
+  if (!aligned(out, 2)) return KNLP_ERR_ALIGN;
   const int ns = (max_context + split_tokens - 1) / split_tokens;
   const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
   if (workspace == nullptr || workspace_bytes < need) return KNLP_ERR_WORKSPACE;
@@ -257,8 +258,8 @@ int knlp_kv_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
                    int32_t max_context, float softmax_scale, int32_t split_tokens,
                    void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
                    int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
-  if (out == nullptr) return KNLP_ERR_ARG;
   if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  if (num_seqs > 0 && out == nullptr) return KNLP_ERR_ARG;
   int st = knlp_kv_decode_partial(query, q_dtype, q_stride_seq, q_stride_head, num_seqs,
                                   num_q_heads, num_kv_heads, head_size, key_cache, value_cache,
                                   block_table, bt_stride_seq, seq_lens, block_size, max_context,

@@ -164,6 +164,8 @@ def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, 
     num_seqs, num_heads, _ = query.shape
     if num_heads % num_kv_heads:
         raise ValueError("num_heads must be a multiple of num_kv_heads")
+    if num_seqs == 0:
+        return torch.empty_like(query)
     if block_table.dtype != torch.int32:
         block_table = block_table.to(torch.int32)
     if block_table.stride(1) != 1:
