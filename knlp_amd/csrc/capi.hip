@@ -45,6 +45,27 @@ int check_plane(const knlp_kv_plane* P, int head_size, bool decode) {
   return KNLP_OK;
 }
 
+// The MFMA decode reads D/8 bytes of codes and D/G fp16 scales per lane with
+// single vector loads and takes one page per 16-token sub-tile.
+bool mfma_layout_ok(const knlp_kv_plane& P, int head_size, int block_size) {
+  if (block_size % 16) return false;
+  const int64_t lb = head_size / 8;
+  const int64_t sb = 2 * (head_size / P.group_size);
+  const auto strides_ok = [](int64_t a, int64_t b, int64_t c, int64_t m) {
+    return a % m == 0 && b % m == 0 && c % m == 0;
+  };
+  if (!aligned(P.data, lb) || !strides_ok(P.stride_block, P.stride_page, P.stride_head, lb))
+    return false;
+  if (!aligned(P.scales, sb) ||
+      !strides_ok(2 * P.s_stride_block, 2 * P.s_stride_page, 2 * P.s_stride_head, sb))
+    return false;
+  if (P.format == KNLP_KV_INT4_ASYM &&
+      (!aligned(P.zeros, sb) ||
+       !strides_ok(2 * P.z_stride_block, 2 * P.z_stride_page, 2 * P.z_stride_head, sb)))
+    return false;
+  return true;
+}
+
 int check_head_size(int head_size) {
   return (head_size == 32 || head_size == 64 || head_size == 128 || head_size == 256)
              ? KNLP_OK
@@ -224,7 +245,9 @@ int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kind == 1) return launch_decode_mfma(a, head_size, s);
+  if (kind == 1 && mfma_layout_ok(*key_cache, head_size, block_size) &&
+      mfma_layout_ok(*value_cache, head_size, block_size))
+    return launch_decode_mfma(a, head_size, s);
   return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), s);
 }
 

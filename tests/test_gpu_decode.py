@@ -198,6 +198,13 @@ def test_empty_batch_is_noop():
     assert out.shape == (0, 32, 128)
 
 
-def test_kernel_kind_reported():
-    kind = K.decode_kernel_kind(32, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32)
-    assert kind in ("mfma", "valu")
+def test_kernel_kind_dispatch():
+    """The benchmark shapes take the matrix-core kernel; others the VALU one."""
+    kk = K.decode_kernel_kind
+    assert kk(32, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "mfma"
+    assert kk(32, 8, 128, _lib.KV_INT4_SYM, 64, _lib.KV_INT4_SYM, 64) == "mfma"
+    assert kk(12, 12, 64, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "mfma"
+    assert kk(32, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32,
+              torch.bfloat16) == "valu"
+    assert kk(64, 8, 256, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "valu"
+    assert kk(40, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT4_ASYM, 32) == "valu"
