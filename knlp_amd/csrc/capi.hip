@@ -48,7 +48,7 @@ int check_plane(const knlp_kv_plane* P, int head_size, bool decode) {
 // The MFMA decode reads D/8 bytes of codes and D/G fp16 scales per lane with
 // single vector loads and takes one page per 16-token sub-tile.
 bool mfma_layout_ok(const knlp_kv_plane& P, int head_size, int block_size) {
-  if (block_size % 16) return false;
+  if (block_size < 16 || !is_pow2(block_size)) return false;
   const int64_t lb = head_size / 8;
   const int64_t sb = 2 * (head_size / P.group_size);
   const auto strides_ok = [](int64_t a, int64_t b, int64_t c, int64_t m) {
@@ -239,13 +239,14 @@ int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_
   a.bt_stride = bt_stride_seq;
   a.seq_lens = seq_lens;
   a.block_size = block_size;
+  a.block_shift = is_pow2(block_size) ? __builtin_ctz(block_size) : -1;
   a.split_tokens = split_tokens;
   a.num_splits = ns;
   a.max_context = max_context;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kind == 1 && mfma_layout_ok(*key_cache, head_size, block_size) &&
+  if (kind == 1 && softmax_scale > 0.0f && mfma_layout_ok(*key_cache, head_size, block_size) &&
       mfma_layout_ok(*value_cache, head_size, block_size))
     return launch_decode_mfma(a, head_size, s);
   return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), s);

@@ -23,6 +23,7 @@ struct DecodeArgs {
   int64_t bt_stride;
   const int32_t* seq_lens;
   int block_size;
+  int block_shift;          // log2(block_size) when it is a power of two, else -1
   int split_tokens, num_splits;
   int max_context;          // block-table width * block_size; longer seq_lens are clamped
   float scale_log2;         // softmax_scale * log2(e)

@@ -51,6 +51,16 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int i4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// Raw buffer resource over [base, base + 4 GiB): every cache load is
+// "scalar descriptor + 32-bit lane byte offset", so the address arithmetic of
+// a load is scalar.  Word 3 is the gfx9-family raw-buffer format
+// (0x00020000, as composable_kernel's CK_BUFFER_RESOURCE_3RD_DWORD).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(0xFFFFFFFFu), 0x00020000);
+}
 
 constexpr float kRescaleLog2 = 2.0f;
 // slot e of a converted K dword -> nibble index within the dword
@@ -81,14 +91,23 @@ __device__ __forceinline__ float row_sum16(float x) {
 // 8 nibbles (one dword, element 2i in the low nibble of byte i) -> 8 exact
 // fp16 values 16 + n in slot order kNibK.  fp16 0x4C00 is 16.0; the nibble
 // goes to mantissa bits 6..9.
-__device__ __forceinline__ h8 nibbles_to_h8_b16(uint32_t w) {
-  const uint32_t m = 0x03C003C0u, c = 0x4C004C00u;
+// The mask and the 16.0 pattern are kept in VGPRs (see vgpr_const) so that
+// each output is one shift plus one v_and_or_b32: a gfx9 VOP3 instruction
+// cannot take two literal constants.
+__device__ __forceinline__ h8 nibbles_to_h8_b16(uint32_t w, uint32_t m, uint32_t c) {
   u4 o;
   o[0] = ((w << 6) & m) | c;   // n0, n4
   o[1] = ((w << 2) & m) | c;   // n1, n5
   o[2] = ((w >> 2) & m) | c;   // n2, n6
   o[3] = ((w >> 6) & m) | c;   // n3, n7
   return __builtin_bit_cast(h8, o);
+}
+
+// A constant materialised in a VGPR the compiler cannot fold away.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
 }
 
 // nibbles of one dword as 8 int8 slots: [n0 n2 n4 n6 | n1 n3 n5 n7]
@@ -108,19 +127,25 @@ template <>
 struct Halves<4> {
   uint2 v;
   __device__ float get(int i) const { return h2f((i < 2 ? v.x : v.y) >> (16 * (i & 1))); }
-  __device__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint2*>(p); }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  }
 };
 template <>
 struct Halves<2> {
   uint32_t v;
   __device__ float get(int i) const { return h2f(v >> (16 * i)); }
-  __device__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint32_t*>(p); }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  }
 };
 template <>
 struct Halves<1> {
   uint32_t v;
   __device__ float get(int) const { return h2f(v); }
-  __device__ void load(const uint16_t* p) { v = *p; }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+  }
 };
 
 template <int NCH>
@@ -129,172 +154,129 @@ template <>
 struct Codes<4> {
   uint4 v;
   __device__ uint32_t dw(int c) const { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
-  __device__ void load(const uint8_t* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  }
 };
 template <>
 struct Codes<2> {
   uint2 v;
   __device__ uint32_t dw(int c) const { return c == 0 ? v.x : v.y; }
-  __device__ void load(const uint8_t* p) { v = *reinterpret_cast<const uint2*>(p); }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  }
 };
 
 template <int NCH, int NG>
 struct SubTile {
   Codes<NCH> k, v;
   Halves<NG> ks, kz, vs, vz;
-  bool valid;    // this lane's token is inside [t_begin, t_end)
 };
 
-template <int D, int NG>
-__device__ __forceinline__ void load_sub(const DecodeArgs& a, const int32_t* bt, int kvh,
-                                         int base, int t_first, int t_end, int col, int blk,
-                                         bool kasym, bool vasym, SubTile<D / 32, NG>& st) {
-  constexpr int LB = D / 8;      // bytes of codes per lane per token
-  // a sub-tile wholly past the end re-reads the split's first page (masked)
-  const bool sub_valid = base < t_end;
-  const int pbase = sub_valid ? base : t_first;
-  const int64_t page = bt[pbase / a.block_size];
-  const int64_t off = pbase % a.block_size + col;
-  st.valid = sub_valid && (base + col) < t_end;
-  const knlp_kv_plane& K = a.kp;
-  const knlp_kv_plane& V = a.vp;
-  st.k.load(static_cast<const uint8_t*>(K.data) + page * K.stride_block + off * K.stride_page +
-            kvh * K.stride_head + LB * blk);
-  st.v.load(static_cast<const uint8_t*>(V.data) + page * V.stride_block + off * V.stride_page +
-            kvh * V.stride_head + LB * blk);
-  st.ks.load(static_cast<const uint16_t*>(K.scales) + page * K.s_stride_block +
-             off * K.s_stride_page + kvh * K.s_stride_head);
-  st.vs.load(static_cast<const uint16_t*>(V.scales) + page * V.s_stride_block +
-             off * V.s_stride_page + kvh * V.s_stride_head);
-  if (kasym)
-    st.kz.load(static_cast<const uint16_t*>(K.zeros) + page * K.z_stride_block +
-               off * K.z_stride_page + kvh * K.z_stride_head);
-  if (vasym)
-    st.vz.load(static_cast<const uint16_t*>(V.zeros) + page * V.z_stride_block +
-               off * V.z_stride_page + kvh * V.z_stride_head);
+// Per-wave addressing: uniform bases (this kv head folded in) plus
+// loop-invariant per-lane offsets, so every load is "scalar base + vector
+// offset" and the per-tile work is one scalar page lookup.
+struct Addr {
+  const uint8_t* kc;
+  const uint8_t* vc;
+  const uint16_t* ks;
+  const uint16_t* kz;
+  const uint16_t* vs;
+  const uint16_t* vz;
+  int64_t kc_b, kc_p, vc_b, vc_p;       // bytes per block / per page slot
+  int64_t ks_b, ks_p, kz_b, kz_p, vs_b, vs_p, vz_b, vz_p;   // halves
+  uint32_t lkc, lvc;                    // lane byte offsets of the codes
+  uint32_t lks, lkz, lvs, lvz;          // lane byte offsets of scales / zeros
+  const int32_t* bt;
+  int bs_shift;
+};
+
+// Page lookup: lane l of `win` holds block_table[seq, win_first + l]; the
+// sub-tile's page is read back with v_readlane into an SGPR, so all address
+// arithmetic of a load is scalar.  The window is refilled every 64 pages.
+struct PageWindow {
+  int win;          // per lane
+  int first;        // uniform: block-table index held by lane 0
+  int last;         // uniform: last block-table index this split touches
+  __device__ __forceinline__ void fill(const int32_t* bt, int lane, int first_idx) {
+    first = first_idx;
+    const int idx = first_idx + lane;
+    win = idx <= last ? bt[idx] : 0;
+  }
+  __device__ __forceinline__ int64_t page(const int32_t* bt, int lane, int idx) {
+    if (idx - first >= kWave) fill(bt, lane, idx);      // uniform branch
+    return static_cast<int64_t>(__builtin_amdgcn_readlane(win, idx - first));
+  }
+};
+
+template <int NCH, int NG, bool KASYM, bool VASYM>
+__device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane, int pbase,
+                                         SubTile<NCH, NG>& st) {
+  const int64_t page = P.page(A.bt, lane, pbase >> A.bs_shift);
+  const int64_t off0 = pbase & ((1 << A.bs_shift) - 1);
+  st.k.load(rsrc_of(A.kc + (page * A.kc_b + off0 * A.kc_p)), A.lkc);
+  st.v.load(rsrc_of(A.vc + (page * A.vc_b + off0 * A.vc_p)), A.lvc);
+  st.ks.load(rsrc_of(A.ks + (page * A.ks_b + off0 * A.ks_p)), A.lks);
+  st.vs.load(rsrc_of(A.vs + (page * A.vs_b + off0 * A.vs_p)), A.lvs);
+  if constexpr (KASYM) st.kz.load(rsrc_of(A.kz + (page * A.kz_b + off0 * A.kz_p)), A.lkz);
+  if constexpr (VASYM) st.vz.load(rsrc_of(A.vz + (page * A.vz_b + off0 * A.vz_p)), A.lvz);
 }
 
-template <int D, int NG>
-__global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
-  constexpr int NCH = D / 32;    // K-chunks of 32 along head_dim = dwords per lane
-  constexpr int GPL = 4 / NG;    // q heads per lane (rows 4blk..4blk+3)
-  const int lane = threadIdx.x & (kWave - 1);
-  const int col = lane & 15;
-  const int blk = lane >> 4;
-  const int wave = threadIdx.x / kWave;
-  const int hpb = blockDim.x / kWave;
-  const int split = blockIdx.x;
-  const int seq = blockIdx.y;
-  const int kvh = blockIdx.z * hpb + wave;
-  if (kvh >= a.num_kv_heads) return;
-  const int seq_len = min(a.seq_lens[seq], a.max_context);
-  const int t_begin = split * a.split_tokens;
-  if (t_begin >= seq_len) return;
-  const int t_end = min(seq_len, t_begin + a.split_tokens);
-  const int G = a.group;
-  const int gs = a.kp.group_size;
-  const int rows = G * NG;
-  const bool kasym = a.kp.format == KNLP_KV_INT4_ASYM;
-  const bool vasym = a.vp.format == KNLP_KV_INT4_ASYM;
+// Running state of one wave.
+template <int NCH, int NG, bool KASYM, bool VASYM>
+struct WaveState {
+  static constexpr int GPL = 4 / NG;
+  h8 aq[NCH];          // masked q, A operands of QK (row = col)
+  float qsum[4];       // sum of q over the group of rows 4blk..4blk+3
+  f4 cinit;            // QK accumulator start: cancels the 16 bias (and the -8 of sym K)
+  h4 eye;              // identity, B operand of the P' transpose
+  long vsel[2];        // 64 * selection, B operand of the V transpose
+  f4 acc[NCH][2];      // PV accumulators, rows (g, vg) x columns d
+  float m_run[GPL];    // running max per q head (unscaled score units)
+  float lsum[GPL];     // per-lane partial softmax sums
+  float zacc[4];       // per-lane sum_t p * (z - 16 s), rows 4blk + e
+  float sl2;           // softmax_scale * log2(e)
+  float thr;           // rescale threshold 2 / sl2 (unscaled units)
+  uint32_t nib_mask;   // 0x03C003C0 in a VGPR
+  uint32_t nib_bias;   // 0x4C004C00 (fp16 16.0 twice) in a VGPR
 
-  // ---- masked q: A operands of QK; row r = col ------------------------------
-  h8 aq[NCH];
-  float qpart = 0.0f;
-  {
-    const int r = col;
-    const bool rv = r < rows;
-    const int g = rv ? r / NG : 0;
-    const int kg = r % NG;
-    const uint16_t* qrow = a.q + seq * a.q_stride_seq + (kvh * G + g) * a.q_stride_head;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = (D / 4) * blk + 8 * c + kNibK[e];
-        _Float16 v = 0;
-        if (rv && d / gs == kg) v = __builtin_bit_cast(_Float16, qrow[d]);
-        aq[c][e] = v;
-        qpart += static_cast<float>(v);
-      }
+  template <bool MASK>
+  __device__ __forceinline__ void step(const SubTile<NCH, NG> (&st)[2], int tbase, int t_end,
+                                       int col) {
+    bool valid[2] = {true, true};
+    if constexpr (MASK) {
+      valid[0] = tbase + col < t_end;
+      valid[1] = tbase + 16 + col < t_end;
     }
-  }
-  // sum of q over row r's group, then spread so lane (t, blk) has rows 4blk+i
-  qpart += __shfl_xor(qpart, 16, kWave);
-  qpart += __shfl_xor(qpart, 32, kWave);
-  float qsum[4];
-  f4 cinit;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    qsum[i] = __shfl(qpart, 4 * blk + i, kWave);
-    cinit[i] = -16.0f * qsum[i];
-  }
-  // identity (P' transpose) and 64 * selection (V transpose) operands
-  h4 eye;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) eye[e] = (blk == col / 4 && e == col % 4) ? 1.0f : 0.0f;
-  long vsel[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    vsel[h] = blk == col / 4 ? static_cast<long>(64ull << (8 * (4 * h + col % 4))) : 0l;
-  const i4 vinit = {0x4C00, 0x4C00, 0x4C00, 0x4C00};
-
-  f4 acc[NCH][2];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) acc[c][0] = acc[c][1] = f4{0.f, 0.f, 0.f, 0.f};
-  float m_run[GPL], lsum[GPL], zacc[4];
-#pragma unroll
-  for (int i = 0; i < GPL; ++i) {
-    m_run[i] = -INFINITY;
-    lsum[i] = 0.0f;
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) zacc[e] = 0.0f;
-
-  const int32_t* bt = a.block_table + seq * a.bt_stride;
-  const float sl2 = a.scale_log2;
-
-  SubTile<NCH, NG> cur[2], nxt[2];
-  load_sub<D, NG>(a, bt, kvh, t_begin, t_begin, t_end, col, blk, kasym, vasym, cur[0]);
-  load_sub<D, NG>(a, bt, kvh, t_begin + 16, t_begin, t_end, col, blk, kasym, vasym, cur[1]);
-
-  for (int t0 = t_begin; t0 < t_end; t0 += 32) {
-    const bool more = t0 + 32 < t_end;
-    if (more) {
-      load_sub<D, NG>(a, bt, kvh, t0 + 32, t_begin, t_end, col, blk, kasym, vasym, nxt[0]);
-      load_sub<D, NG>(a, bt, kvh, t0 + 48, t_begin, t_end, col, blk, kasym, vasym, nxt[1]);
-    }
-
-    // ---- scores ---------------------------------------------------------------
+    // ---- scores (unscaled): sum_kg s * sum(q.n) + z * sum(q) ----------------
     float score[2][GPL];
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       f4 S = cinit;
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[c], nibbles_to_h8_b16(cur[x].k.dw(c)), S,
-                                                   0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            aq[c], nibbles_to_h8_b16(st[x].k.dw(c), nib_mask, nib_bias), S, 0, 0, 0);
 #pragma unroll
       for (int gi = 0; gi < GPL; ++gi) {
         float sc = 0.0f;
 #pragma unroll
         for (int kg = 0; kg < NG; ++kg) {
           const int i = gi * NG + kg;
-          const float s = cur[x].ks.get(kg);
-          const float z = kasym ? cur[x].kz.get(kg) : -8.0f * s;
-          sc = fmaf(s, S[i], fmaf(z, qsum[i], sc));
+          if constexpr (KASYM) sc = fmaf(st[x].kz.get(kg), qsum[i], sc);
+          sc = fmaf(st[x].ks.get(kg), S[i], sc);
         }
-        score[x][gi] = cur[x].valid ? sc * sl2 : -INFINITY;
+        score[x][gi] = (MASK && !valid[x]) ? -INFINITY : sc;
       }
     }
-
-    // ---- online softmax (lazy max) -------------------------------------------
+    // ---- lazy online-softmax max --------------------------------------------
     float alpha[GPL];
     bool need = false;
 #pragma unroll
     for (int gi = 0; gi < GPL; ++gi) {
       const float tmax = row_max16(fmaxf(score[0][gi], score[1][gi]));
-      const bool up = tmax > m_run[gi] + kRescaleLog2;
-      alpha[gi] = up ? exp2f(m_run[gi] - tmax) : 1.0f;
+      const bool up = tmax > m_run[gi] + thr;
+      alpha[gi] = up ? __builtin_amdgcn_exp2f((m_run[gi] - tmax) * sl2) : 1.0f;
       m_run[gi] = up ? tmax : m_run[gi];
       need |= up;
     }
@@ -310,45 +292,52 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[c][h][i] *= alpha[i / NG];
     }
-
-    // ---- P' = p * s_v (hi + lo), zero-point term, transposes -----------------
+    // ---- P' = p * s_v (fp16 hi + lo), zero term, P' transpose ---------------
     h8 ahi, alo;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       float p[GPL];
 #pragma unroll
       for (int gi = 0; gi < GPL; ++gi) {
-        p[gi] = exp2f(score[x][gi] - m_run[gi]);
+        // (score - max) first: the token that sets the max gets p = 1 exactly
+        p[gi] = __builtin_amdgcn_exp2f((score[x][gi] - m_run[gi]) * sl2);   // 0 when masked
         lsum[gi] += p[gi];
       }
       h4 xhi, xlo;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int vg = e % NG;
-        const float sv = cur[x].vs.get(vg);
-        const float zv = vasym ? cur[x].vz.get(vg) : -8.0f * sv;
+        float sv = st[x].vs.get(vg);
+        float zv = VASYM ? st[x].vz.get(vg) : -8.0f * sv;
+        if constexpr (MASK) {       // garbage scales past the end must not reach NaN
+          sv = valid[x] ? sv : 0.0f;
+          zv = valid[x] ? zv : 0.0f;
+        }
         const float pe = p[e / NG];
-        const float P = cur[x].valid ? pe * sv : 0.0f;
+        const float P = pe * sv;
         const _Float16 hi = static_cast<_Float16>(P);
         xhi[e] = hi;
-        xlo[e] = static_cast<_Float16>(P - static_cast<float>(hi));
-        zacc[e] = cur[x].valid ? fmaf(pe, fmaf(-16.0f, sv, zv), zacc[e]) : zacc[e];
+        xlo[e] = static_cast<_Float16>(fmaf(pe, sv, -static_cast<float>(hi)));
+        zacc[e] = fmaf(pe, fmaf(-16.0f, sv, zv), zacc[e]);
       }
       const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
       const f4 thi = __builtin_amdgcn_mfma_f32_16x16x16f16(xhi, eye, zero4, 0, 0, 0);
       const f4 tlo = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo, eye, zero4, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        ahi[4 * x + r] = static_cast<_Float16>(thi[r]);
-        alo[4 * x + r] = static_cast<_Float16>(tlo[r]);
-      }
+      const h2 h01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(thi[0], thi[1]));
+      const h2 h23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(thi[2], thi[3]));
+      const h2 l01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(tlo[0], tlo[1]));
+      const h2 l23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(tlo[2], tlo[3]));
+      ahi[4 * x + 0] = h01[0]; ahi[4 * x + 1] = h01[1];
+      ahi[4 * x + 2] = h23[0]; ahi[4 * x + 3] = h23[1];
+      alo[4 * x + 0] = l01[0]; alo[4 * x + 1] = l01[1];
+      alo[4 * x + 2] = l23[0]; alo[4 * x + 3] = l23[1];
     }
-
-    // ---- V transposes and PV ---------------------------------------------------
+    // ---- V transposes and PV ------------------------------------------------
+    const i4 vinit = {0x4C00, 0x4C00, 0x4C00, 0x4C00};
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const long va = nibbles_to_i8x8(cur[0].v.dw(c));
-      const long vb = nibbles_to_i8x8(cur[1].v.dw(c));
+      const long va = nibbles_to_i8x8(st[0].v.dw(c));
+      const long vb = nibbles_to_i8x8(st[1].v.dw(c));
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const i4 ta = __builtin_amdgcn_mfma_i32_16x16x32_i8(va, vsel[h], vinit, 0, 0, 0);
@@ -363,17 +352,150 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
         acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
       }
     }
-    if (more) {
-      cur[0] = nxt[0];
-      cur[1] = nxt[1];
+  }
+};
+
+template <int D, int NG, bool KASYM, bool VASYM>
+__global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
+  constexpr int NCH = D / 32;    // K-chunks of 32 along head_dim = dwords per lane
+  constexpr int LB = D / 8;      // bytes of codes per lane per token
+  constexpr int GPL = 4 / NG;    // q heads per lane (rows 4blk..4blk+3)
+  const int lane = threadIdx.x & (kWave - 1);
+  const int col = lane & 15;
+  const int blk = lane >> 4;
+  // the wave index is uniform; readfirstlane lets the compiler keep every
+  // per-head base address in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  const int hpb = blockDim.x / kWave;
+  const int split = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int kvh = blockIdx.z * hpb + wave;
+  if (kvh >= a.num_kv_heads) return;
+  const int seq_len = min(a.seq_lens[seq], a.max_context);
+  const int t_begin = split * a.split_tokens;
+  if (t_begin >= seq_len) return;
+  const int t_end = min(seq_len, t_begin + a.split_tokens);
+  const int G = a.group;
+  const int gs = a.kp.group_size;
+  const int rows = G * NG;
+
+  WaveState<NCH, NG, KASYM, VASYM> W;
+  // ---- masked q (row r = col): this lane's D/4 consecutive elements ----------
+  float qpart = 0.0f;
+  {
+    const int r = col;
+    const int g = r < rows ? r / NG : 0;
+    const bool on = r < rows && ((D / 4) * blk) / gs == r % NG;
+    const uint16_t* qp = a.q + seq * a.q_stride_seq + (kvh * G + g) * a.q_stride_head + (D / 4) * blk;
+    uint16_t qv[D / 4];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const uint4 w = reinterpret_cast<const uint4*>(qp)[i];
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qv[8 * i + 2 * j] = static_cast<uint16_t>(ws[j]);
+        qv[8 * i + 2 * j + 1] = static_cast<uint16_t>(ws[j] >> 16);
+      }
     }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 v = on ? __builtin_bit_cast(_Float16, qv[8 * c + kNibK[e]]) : _Float16(0);
+        W.aq[c][e] = v;
+        qpart += static_cast<float>(v);
+      }
+    }
+  }
+  qpart += __shfl_xor(qpart, 16, kWave);
+  qpart += __shfl_xor(qpart, 32, kWave);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    W.qsum[i] = __shfl(qpart, 4 * blk + i, kWave);
+    W.cinit[i] = (KASYM ? -16.0f : -24.0f) * W.qsum[i];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) W.eye[e] = (blk == col / 4 && e == col % 4) ? 1.0f : 0.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    W.vsel[h] = blk == col / 4 ? static_cast<long>(64ull << (8 * (4 * h + col % 4))) : 0l;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) W.acc[c][0] = W.acc[c][1] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < GPL; ++i) {
+    W.m_run[i] = -INFINITY;
+    W.lsum[i] = 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) W.zacc[e] = 0.0f;
+  W.sl2 = a.scale_log2;
+  W.thr = kRescaleLog2 / a.scale_log2;
+  W.nib_mask = vgpr_const(0x03C003C0u);
+  W.nib_bias = vgpr_const(0x4C004C00u);
+
+  Addr A;
+  {
+    const knlp_kv_plane& K = a.kp;
+    const knlp_kv_plane& V = a.vp;
+    A.kc = static_cast<const uint8_t*>(K.data) + kvh * K.stride_head;
+    A.vc = static_cast<const uint8_t*>(V.data) + kvh * V.stride_head;
+    A.ks = static_cast<const uint16_t*>(K.scales) + kvh * K.s_stride_head;
+    A.vs = static_cast<const uint16_t*>(V.scales) + kvh * V.s_stride_head;
+    A.kz = KASYM ? static_cast<const uint16_t*>(K.zeros) + kvh * K.z_stride_head : nullptr;
+    A.vz = VASYM ? static_cast<const uint16_t*>(V.zeros) + kvh * V.z_stride_head : nullptr;
+    A.kc_b = K.stride_block; A.kc_p = K.stride_page;
+    A.vc_b = V.stride_block; A.vc_p = V.stride_page;
+    A.ks_b = K.s_stride_block; A.ks_p = K.s_stride_page;
+    A.vs_b = V.s_stride_block; A.vs_p = V.s_stride_page;
+    A.kz_b = K.z_stride_block; A.kz_p = K.z_stride_page;
+    A.vz_b = V.z_stride_block; A.vz_p = V.z_stride_page;
+    A.lkc = static_cast<uint32_t>(col * K.stride_page + LB * blk);
+    A.lvc = static_cast<uint32_t>(col * V.stride_page + LB * blk);
+    A.lks = static_cast<uint32_t>(2 * col * K.s_stride_page);
+    A.lvs = static_cast<uint32_t>(2 * col * V.s_stride_page);
+    A.lkz = static_cast<uint32_t>(2 * col * K.z_stride_page);
+    A.lvz = static_cast<uint32_t>(2 * col * V.z_stride_page);
+    A.bt = a.block_table + seq * a.bt_stride;
+    A.bs_shift = a.block_shift;
+  }
+
+  PageWindow PW;
+  PW.last = (t_end - 1) >> A.bs_shift;
+  PW.fill(A.bt, lane, t_begin >> A.bs_shift);
+
+  // 32-token tiles in order through a two-buffer pipeline: the loads of tile
+  // i + 1 are in flight while tile i computes.  Only a sequence's last split
+  // can end in a partial tile; that one runs the masked step.  Tiles are
+  // visited in increasing order so the page window only moves forward.
+  const int ntiles = (t_end - t_begin + 31) / 32;
+  SubTile<NCH, NG> X[2], Y[2];
+  auto load_tile = [&](int tb, SubTile<NCH, NG>(&buf)[2]) {
+    load_sub<NCH, NG, KASYM, VASYM>(A, PW, lane, tb, buf[0]);
+    // a second half wholly past the end re-reads the first half's page (masked)
+    load_sub<NCH, NG, KASYM, VASYM>(A, PW, lane, tb + 16 < t_end ? tb + 16 : tb, buf[1]);
+  };
+  auto run_tile = [&](int tb, const SubTile<NCH, NG>(&buf)[2]) {
+    if (tb + 32 <= t_end)
+      W.template step<false>(buf, tb, t_end, col);
+    else
+      W.template step<true>(buf, tb, t_end, col);
+  };
+  load_tile(t_begin, X);
+  for (int i = 0; i < ntiles; i += 2) {
+    const int tb = t_begin + 32 * i;
+    if (i + 1 < ntiles) load_tile(tb + 32, Y);
+    run_tile(tb, X);
+    if (i + 1 >= ntiles) break;
+    if (i + 2 < ntiles) load_tile(tb + 64, X);
+    run_tile(tb + 32, Y);
   }
 
   // ---- reduce over tokens and write the partial ---------------------------------
 #pragma unroll
-  for (int gi = 0; gi < GPL; ++gi) lsum[gi] = row_sum16(lsum[gi]);
+  for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) zacc[e] = row_sum16(zacc[e]);
+  for (int e = 0; e < 4; ++e) W.zacc[e] = row_sum16(W.zacc[e]);
   const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * G;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -386,7 +508,7 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
         const int g = r / NG;
         if (g < G && d / gs == r % NG) {
           const int64_t row = (row0 + g) * a.num_splits + split;
-          a.part_o[row * D + d] = acc[c][h][i] + zacc[i];
+          a.part_o[row * D + d] = W.acc[c][h][i] + W.zacc[i];
         }
       }
     }
@@ -397,8 +519,8 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
       const int g = (4 * blk) / NG + gi;
       if (g < G) {
         const int64_t row = (row0 + g) * a.num_splits + split;
-        a.part_ml[2 * row] = m_run[gi];
-        a.part_ml[2 * row + 1] = lsum[gi];
+        a.part_ml[2 * row] = W.m_run[gi] * W.sl2;
+        a.part_ml[2 * row + 1] = W.lsum[gi];
       }
     }
   }
@@ -428,10 +550,19 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
   const dim3 block(kWave * hpb);
   const int ng = head_size / a.kp.group_size;
-#define KNLP_MFMA(D, NG)                                                               \
-  if (head_size == D && ng == NG) {                                                    \
-    hipLaunchKernelGGL((decode_mfma_kernel<D, NG>), grid, block, 0, stream, a);        \
-    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                \
+  const bool ka = a.kp.format == KNLP_KV_INT4_ASYM;
+  const bool va = a.vp.format == KNLP_KV_INT4_ASYM;
+#define KNLP_MFMA(D, NG)                                                                \
+  if (head_size == D && ng == NG) {                                                     \
+    if (ka && va)                                                                       \
+      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, true, true>), grid, block, 0, stream, a);   \
+    else if (ka)                                                                        \
+      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, true, false>), grid, block, 0, stream, a);  \
+    else if (va)                                                                        \
+      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, true>), grid, block, 0, stream, a);  \
+    else                                                                                \
+      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, false>), grid, block, 0, stream, a); \
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                 \
   }
   KNLP_MFMA(128, 4)
   KNLP_MFMA(128, 2)
