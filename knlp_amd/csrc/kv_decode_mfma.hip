@@ -355,31 +355,16 @@ struct WaveState {
   }
 };
 
+// q, constants and accumulators of the wave serving kv head `kvh`.
 template <int D, int NG, bool KASYM, bool VASYM>
-__global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
-  constexpr int NCH = D / 32;    // K-chunks of 32 along head_dim = dwords per lane
-  constexpr int LB = D / 8;      // bytes of codes per lane per token
-  constexpr int GPL = 4 / NG;    // q heads per lane (rows 4blk..4blk+3)
-  const int lane = threadIdx.x & (kWave - 1);
-  const int col = lane & 15;
-  const int blk = lane >> 4;
-  // the wave index is uniform; readfirstlane lets the compiler keep every
-  // per-head base address in SGPRs
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int hpb = blockDim.x / kWave;
-  const int split = blockIdx.x;
-  const int seq = blockIdx.y;
-  const int kvh = blockIdx.z * hpb + wave;
-  if (kvh >= a.num_kv_heads) return;
-  const int seq_len = min(a.seq_lens[seq], a.max_context);
-  const int t_begin = split * a.split_tokens;
-  if (t_begin >= seq_len) return;
-  const int t_end = min(seq_len, t_begin + a.split_tokens);
+__device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W,
+                                          const DecodeArgs& a, int seq, int kvh, int col,
+                                          int blk) {
+  constexpr int NCH = D / 32;
+  constexpr int GPL = 4 / NG;
   const int G = a.group;
   const int gs = a.kp.group_size;
   const int rows = G * NG;
-
-  WaveState<NCH, NG, KASYM, VASYM> W;
   // ---- masked q (row r = col): this lane's D/4 consecutive elements ----------
   float qpart = 0.0f;
   {
@@ -433,6 +418,75 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   W.thr = kRescaleLog2 / a.scale_log2;
   W.nib_mask = vgpr_const(0x03C003C0u);
   W.nib_bias = vgpr_const(0x4C004C00u);
+}
+
+// Reduce over tokens and write the wave's partial (acc, max, sum).
+template <int D, int NG, bool KASYM, bool VASYM>
+__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM>& W,
+                                               const DecodeArgs& a, int seq, int kvh,
+                                               int split, int col, int blk) {
+  constexpr int NCH = D / 32;
+  constexpr int GPL = 4 / NG;
+  const int G = a.group;
+  const int gs = a.kp.group_size;
+#pragma unroll
+  for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) W.zacc[e] = row_sum16(W.zacc[e]);
+  const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * G;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int d = (D / 4) * (col / 4) + 8 * c + 2 * (col % 4) + h;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * blk + i;
+        const int g = r / NG;
+        if (g < G && d / gs == r % NG) {
+          const int64_t row = (row0 + g) * a.num_splits + split;
+          a.part_o[row * D + d] = W.acc[c][h][i] + W.zacc[i];
+        }
+      }
+    }
+  }
+  if (col == 0) {
+#pragma unroll
+    for (int gi = 0; gi < GPL; ++gi) {
+      const int g = (4 * blk) / NG + gi;
+      if (g < G) {
+        const int64_t row = (row0 + g) * a.num_splits + split;
+        a.part_ml[2 * row] = W.m_run[gi] * W.sl2;
+        a.part_ml[2 * row + 1] = W.lsum[gi];
+      }
+    }
+  }
+}
+
+// Per-head loads: each wave fetches its own kv head's rows (any layout that
+// passes the alignment checks).  One wave per (sequence, kv head, split).
+template <int D, int NG, bool KASYM, bool VASYM>
+__global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
+  constexpr int NCH = D / 32;    // K-chunks of 32 along head_dim = dwords per lane
+  constexpr int LB = D / 8;      // bytes of codes per lane per token
+  const int lane = threadIdx.x & (kWave - 1);
+  const int col = lane & 15;
+  const int blk = lane >> 4;
+  // the wave index is uniform; readfirstlane lets the compiler keep every
+  // per-head base address in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  const int hpb = blockDim.x / kWave;
+  const int split = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int kvh = blockIdx.z * hpb + wave;
+  if (kvh >= a.num_kv_heads) return;
+  const int seq_len = min(a.seq_lens[seq], a.max_context);
+  const int t_begin = split * a.split_tokens;
+  if (t_begin >= seq_len) return;
+  const int t_end = min(seq_len, t_begin + a.split_tokens);
+
+  WaveState<NCH, NG, KASYM, VASYM> W;
+  init_wave<D, NG, KASYM, VASYM>(W, a, seq, kvh, col, blk);
 
   Addr A;
   {
@@ -490,40 +544,230 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
     if (i + 2 < ntiles) load_tile(tb + 64, X);
     run_tile(tb + 32, Y);
   }
+  write_partials<D, NG, KASYM, VASYM>(W, a, seq, kvh, split, col, blk);
+}
 
-  // ---- reduce over tokens and write the partial ---------------------------------
+// ---------------------------------------------------------------------------
+// Cooperative page staging, for caches whose kv heads are densely packed in a
+// token row (stride_head = D/2 code bytes and D/G scales) and Hkv % 8 == 0.
+//
+// A block is 8 waves serving 8 consecutive kv heads of one (sequence, split),
+// so each 16-token sub-tile of each array (codes K and V, scales and zeros) is
+// 16 rows of 8 heads' contiguous bytes.  All 512 threads fetch a 32-token tile
+// with 16-byte loads (one wave instruction = 1 KB of consecutive rows), one
+// tile ahead in registers, then store it to LDS with padded rows; after a
+// barrier each wave reads its own head's slice in the lane layout of the
+// per-head kernel.  Per-head loads touch 64-byte fragments at a 512-byte
+// stride and 8-byte scale fragments at a 64-byte stride, which measured
+// 55-59% of HBM peak even without compute; page-contiguous loads measured
+// 82-85%, as fast as a plain stream.
+// ---------------------------------------------------------------------------
+template <int D, int NG>
+struct CoopLayout {
+  static constexpr int kHeads = 8;
+  static constexpr int HB = D / 2;                // code bytes per head and token
+  static constexpr int SB = 2 * NG;               // scale bytes per head and token
+  static constexpr int CPR = kHeads * HB / 16;    // 16-byte chunks per code row
+  static constexpr int NCC = 16 * CPR;            // code chunks per sub-tile
+  static constexpr int CROW = kHeads * HB + 16;   // padded LDS row of codes
+  static constexpr int SROW = kHeads * SB + 8;    // padded LDS row of one scale array
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = 2 * 16 * CROW;
+  static constexpr int S_OFF = 4 * 16 * CROW;     // 4 arrays (ks, vs, kz, vz) x 2 sub-tiles
+  static constexpr int BYTES = S_OFF + 8 * 16 * SROW;
+  static_assert(NCC <= 512, "one code chunk per thread and sub-tile");
+  static_assert(16 * NG <= kWave, "one scale chunk per lane");
+};
+
+// One thread's share of a 32-token tile, in flight between HBM and LDS.
+struct CoopStage {
+  uint4 k[2], v[2];   // code chunk of sub-tile 0 and 1
+  uint4 s;            // scale chunk (array and sub-tile fixed per wave)
+};
+
+// Loop-invariant addressing of the cooperative loader.
+struct CoopAddr {
+  const uint8_t* kc;      // codes of head h0 (block/page strides below)
+  const uint8_t* vc;
+  const uint8_t* sp;      // this wave's scale array, head h0
+  int64_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
+  uint32_t lk, lv, ls;    // lane byte offsets
+  int lds_c, lds_s;       // LDS byte offsets of this thread's chunks
+  bool c_on, s_on;
+  int s_x;                // sub-tile whose scale chunk this wave loads
+  const int32_t* bt;
+  int bs_shift;
+};
+
+template <int D, int NG>
+__device__ __forceinline__ void coop_load(const CoopAddr& C, PageWindow& P, int lane, int tb,
+                                          int t_end, CoopStage& R) {
+  int64_t page[2], off[2];
 #pragma unroll
-  for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]);
+  for (int x = 0; x < 2; ++x) {
+    // a second half wholly past the end re-reads the first half's page (masked)
+    const int pb = (x == 0 || tb + 16 < t_end) ? tb + 16 * x : tb;
+    page[x] = P.page(C.bt, lane, pb >> C.bs_shift);
+    off[x] = pb & ((1 << C.bs_shift) - 1);
+  }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) W.zacc[e] = row_sum16(W.zacc[e]);
-  const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * G;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int d = (D / 4) * (col / 4) + 8 * c + 2 * (col % 4) + h;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * blk + i;
-        const int g = r / NG;
-        if (g < G && d / gs == r % NG) {
-          const int64_t row = (row0 + g) * a.num_splits + split;
-          a.part_o[row * D + d] = W.acc[c][h][i] + W.zacc[i];
-        }
-      }
+  for (int x = 0; x < 2; ++x) {
+    if (CoopLayout<D, NG>::NCC == 512 || C.c_on) {
+      R.k[x] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+          rsrc_of(C.kc + (page[x] * C.kc_b + off[x] * C.kc_p)), C.lk, 0, 0));
+      R.v[x] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+          rsrc_of(C.vc + (page[x] * C.vc_b + off[x] * C.vc_p)), C.lv, 0, 0));
     }
   }
-  if (col == 0) {
+  if (C.s_on) {
+    const int64_t pg = C.s_x ? page[1] : page[0];
+    const int64_t of = C.s_x ? off[1] : off[0];
+    R.s = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+        rsrc_of(C.sp + (pg * C.sp_b + of * C.sp_p)), C.ls, 0, 0));
+  }
+}
+
+template <int D, int NG>
+__device__ __forceinline__ void coop_store(const CoopAddr& C, uint8_t* buf, const CoopStage& R) {
+  using L = CoopLayout<D, NG>;
+  if (L::NCC == 512 || C.c_on) {
 #pragma unroll
-    for (int gi = 0; gi < GPL; ++gi) {
-      const int g = (4 * blk) / NG + gi;
-      if (g < G) {
-        const int64_t row = (row0 + g) * a.num_splits + split;
-        a.part_ml[2 * row] = W.m_run[gi] * W.sl2;
-        a.part_ml[2 * row + 1] = W.lsum[gi];
-      }
+    for (int x = 0; x < 2; ++x) {
+      *reinterpret_cast<uint4*>(buf + L::K_OFF + x * 16 * L::CROW + C.lds_c) = R.k[x];
+      *reinterpret_cast<uint4*>(buf + L::V_OFF + x * 16 * L::CROW + C.lds_c) = R.v[x];
     }
   }
+  if (C.s_on) {
+    // padded scale rows are 8-byte aligned
+    *reinterpret_cast<uint2*>(buf + C.lds_s) = make_uint2(R.s.x, R.s.y);
+    *reinterpret_cast<uint2*>(buf + C.lds_s + 8) = make_uint2(R.s.z, R.s.w);
+  }
+}
+
+template <int NG>
+__device__ __forceinline__ void halves_from_lds(Halves<NG>& h, const uint8_t* p) {
+  if constexpr (NG == 4)
+    h.v = *reinterpret_cast<const uint2*>(p);
+  else if constexpr (NG == 2)
+    h.v = *reinterpret_cast<const uint32_t*>(p);
+  else
+    h.v = *reinterpret_cast<const uint16_t*>(p);
+}
+
+template <int D, int NG, bool KASYM, bool VASYM>
+__device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col, int blk,
+                                          SubTile<D / 32, NG> (&st)[2]) {
+  using L = CoopLayout<D, NG>;
+  constexpr int LB = D / 8;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int co = x * 16 * L::CROW + col * L::CROW + wave * L::HB + blk * LB;
+    if constexpr (D == 128) {
+      st[x].k.v = *reinterpret_cast<const uint4*>(buf + L::K_OFF + co);
+      st[x].v.v = *reinterpret_cast<const uint4*>(buf + L::V_OFF + co);
+    } else {
+      st[x].k.v = *reinterpret_cast<const uint2*>(buf + L::K_OFF + co);
+      st[x].v.v = *reinterpret_cast<const uint2*>(buf + L::V_OFF + co);
+    }
+    const int so = L::S_OFF + x * 16 * L::SROW + col * L::SROW + wave * L::SB;
+    halves_from_lds<NG>(st[x].ks, buf + so);
+    halves_from_lds<NG>(st[x].vs, buf + so + 1 * 2 * 16 * L::SROW);
+    if constexpr (KASYM) halves_from_lds<NG>(st[x].kz, buf + so + 2 * 2 * 16 * L::SROW);
+    if constexpr (VASYM) halves_from_lds<NG>(st[x].vz, buf + so + 3 * 2 * 16 * L::SROW);
+  }
+}
+
+template <int D, int NG, bool KASYM, bool VASYM>
+__global__ __launch_bounds__(512) void decode_mfma_coop_kernel(DecodeArgs a) {
+  using L = CoopLayout<D, NG>;
+  constexpr int NCH = D / 32;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][L::BYTES];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int col = lane & 15;
+  const int blk = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int split = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int h0 = blockIdx.z * L::kHeads;
+  const int kvh = h0 + wave;
+  // every exit below is uniform over the block: all waves reach every barrier
+  const int seq_len = min(a.seq_lens[seq], a.max_context);
+  const int t_begin = split * a.split_tokens;
+  if (t_begin >= seq_len) return;
+  const int t_end = min(seq_len, t_begin + a.split_tokens);
+
+  WaveState<NCH, NG, KASYM, VASYM> W;
+  init_wave<D, NG, KASYM, VASYM>(W, a, seq, kvh, col, blk);
+
+  CoopAddr C;
+  {
+    const knlp_kv_plane& K = a.kp;
+    const knlp_kv_plane& V = a.vp;
+    C.kc = static_cast<const uint8_t*>(K.data) + h0 * K.stride_head;
+    C.vc = static_cast<const uint8_t*>(V.data) + h0 * V.stride_head;
+    C.kc_b = K.stride_block; C.kc_p = K.stride_page;
+    C.vc_b = V.stride_block; C.vc_p = V.stride_page;
+    const int c_row = tid / L::CPR;
+    const int c_byte = 16 * (tid % L::CPR);
+    C.c_on = tid < L::NCC;
+    C.lk = static_cast<uint32_t>(c_row * K.stride_page + c_byte);
+    C.lv = static_cast<uint32_t>(c_row * V.stride_page + c_byte);
+    C.lds_c = c_row * L::CROW + c_byte;
+    // wave w loads scale array w / 2 (ks, vs, kz, vz) of sub-tile w % 2
+    const int arr = wave >> 1;
+    C.s_x = wave & 1;
+    const uint16_t* base = arr == 0 ? static_cast<const uint16_t*>(K.scales)
+                         : arr == 1 ? static_cast<const uint16_t*>(V.scales)
+                         : arr == 2 ? static_cast<const uint16_t*>(K.zeros)
+                                    : static_cast<const uint16_t*>(V.zeros);
+    const int64_t sh = arr == 0 ? K.s_stride_head : arr == 1 ? V.s_stride_head
+                     : arr == 2 ? K.z_stride_head : V.z_stride_head;
+    const int64_t sbk = arr == 0 ? K.s_stride_block : arr == 1 ? V.s_stride_block
+                      : arr == 2 ? K.z_stride_block : V.z_stride_block;
+    const int64_t spg = arr == 0 ? K.s_stride_page : arr == 1 ? V.s_stride_page
+                      : arr == 2 ? K.z_stride_page : V.z_stride_page;
+    const bool arr_on = arr < 2 || (arr == 2 && KASYM) || (arr == 3 && VASYM);
+    C.s_on = arr_on && lane < 16 * NG;
+    C.sp = arr_on ? reinterpret_cast<const uint8_t*>(base + h0 * sh) : nullptr;
+    C.sp_b = 2 * sbk;
+    C.sp_p = 2 * spg;
+    const int s_row = lane / NG;
+    const int s_byte = 16 * (lane % NG);
+    C.ls = static_cast<uint32_t>(s_row * C.sp_p + s_byte);
+    C.lds_s = L::S_OFF + (arr * 2 + C.s_x) * 16 * L::SROW + s_row * L::SROW + s_byte;
+    C.bt = a.block_table + seq * a.bt_stride;
+    C.bs_shift = a.block_shift;
+  }
+
+  PageWindow PW;
+  PW.last = (t_end - 1) >> C.bs_shift;
+  PW.fill(C.bt, lane, t_begin >> C.bs_shift);
+
+  // Tile i computes from LDS buffer i % 2 while tile i + 1 is in flight in
+  // registers; after the compute it goes to the other buffer and tile i + 2
+  // is requested.  One barrier per tile.
+  const int ntiles = (t_end - t_begin + 31) / 32;
+  CoopStage R;
+  coop_load<D, NG>(C, PW, lane, t_begin, t_end, R);
+  coop_store<D, NG>(C, lds[0], R);
+  if (ntiles > 1) coop_load<D, NG>(C, PW, lane, t_begin + 32, t_end, R);
+  __syncthreads();
+  for (int i = 0; i < ntiles; ++i) {
+    const int tb = t_begin + 32 * i;
+    SubTile<NCH, NG> st[2];
+    coop_read<D, NG, KASYM, VASYM>(lds[i & 1], wave, col, blk, st);
+    if (tb + 32 <= t_end)
+      W.template step<false>(st, tb, t_end, col);
+    else
+      W.template step<true>(st, tb, t_end, col);
+    if (i + 1 < ntiles) {
+      coop_store<D, NG>(C, lds[(i + 1) & 1], R);
+      if (i + 2 < ntiles) coop_load<D, NG>(C, PW, lane, tb + 64, t_end, R);
+    }
+    __syncthreads();
+  }
+  write_partials<D, NG, KASYM, VASYM>(W, a, seq, kvh, split, col, blk);
 }
 
 int heads_per_block_mfma(int num_kv_heads) {
@@ -545,24 +789,51 @@ bool mfma_supported(int group, int head_size, int k_format, int k_gs, int v_form
   return group >= 1 && group * ng <= 16;
 }
 
+// Heads densely packed in a token row, 16-byte aligned rows, Hkv % 8 == 0:
+// the cooperative kernel can fetch 8 heads' rows as one contiguous run.
+static bool coop_layout_ok(const knlp_kv_plane& P, int head_size, int num_kv_heads) {
+  const int64_t ng = head_size / P.group_size;
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (num_kv_heads % 8 != 0) return false;
+  if (!a16(P.data) || P.stride_head != head_size / 2 || P.stride_block % 16 != 0 ||
+      P.stride_page % 16 != 0)
+    return false;
+  const auto scales_ok = [&](const void* p, int64_t sb, int64_t sp, int64_t sh) {
+    return a16(p) && sh == ng && (2 * sb) % 16 == 0 && (2 * sp) % 16 == 0;
+  };
+  if (!scales_ok(P.scales, P.s_stride_block, P.s_stride_page, P.s_stride_head)) return false;
+  if (P.format == KNLP_KV_INT4_ASYM &&
+      !scales_ok(P.zeros, P.z_stride_block, P.z_stride_page, P.z_stride_head))
+    return false;
+  return true;
+}
+
 int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
-  const int hpb = heads_per_block_mfma(a.num_kv_heads);
-  const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
-  const dim3 block(kWave * hpb);
   const int ng = head_size / a.kp.group_size;
   const bool ka = a.kp.format == KNLP_KV_INT4_ASYM;
   const bool va = a.vp.format == KNLP_KV_INT4_ASYM;
-#define KNLP_MFMA(D, NG)                                                                \
-  if (head_size == D && ng == NG) {                                                     \
-    if (ka && va)                                                                       \
-      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, true, true>), grid, block, 0, stream, a);   \
-    else if (ka)                                                                        \
-      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, true, false>), grid, block, 0, stream, a);  \
-    else if (va)                                                                        \
-      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, true>), grid, block, 0, stream, a);  \
-    else                                                                                \
-      hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, false>), grid, block, 0, stream, a); \
-    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                 \
+  const bool coop = coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
+                    coop_layout_ok(a.vp, head_size, a.num_kv_heads);
+  const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
+  const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
+  const dim3 block(kWave * hpb);
+#define KNLP_MFMA_K(KERNEL, D, NG)                                                       \
+  if (ka && va)                                                                          \
+    hipLaunchKernelGGL((KERNEL<D, NG, true, true>), grid, block, 0, stream, a);          \
+  else if (ka)                                                                           \
+    hipLaunchKernelGGL((KERNEL<D, NG, true, false>), grid, block, 0, stream, a);         \
+  else if (va)                                                                           \
+    hipLaunchKernelGGL((KERNEL<D, NG, false, true>), grid, block, 0, stream, a);         \
+  else                                                                                   \
+    hipLaunchKernelGGL((KERNEL<D, NG, false, false>), grid, block, 0, stream, a);
+#define KNLP_MFMA(D, NG)                                                                 \
+  if (head_size == D && ng == NG) {                                                      \
+    if (coop) {                                                                          \
+      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG)                                        \
+    } else {                                                                             \
+      KNLP_MFMA_K(decode_mfma_kernel, D, NG)                                             \
+    }                                                                                    \
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                  \
   }
   KNLP_MFMA(128, 4)
   KNLP_MFMA(128, 2)
@@ -571,6 +842,7 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   KNLP_MFMA(64, 2)
   KNLP_MFMA(64, 1)
 #undef KNLP_MFMA
+#undef KNLP_MFMA_K
   return KNLP_ERR_SHAPE;
 }
 

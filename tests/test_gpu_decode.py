@@ -104,6 +104,9 @@ CASES = [
     ("mha_d128_sym", [300], 8, 8, 128, 0, 0, 32, 32),
     ("g2_d64", [1000], 8, 4, 64, 1, 1, 32, 32),
     ("g1_d256_sym_g64", [333], 4, 4, 256, 0, 0, 64, 64),
+    ("d64_hkv8_g2", [1500, 300], 16, 8, 64, 1, 1, 32, 32),
+    ("g128_d128_hkv16", [700, 129], 64, 16, 128, 1, 1, 128, 128),
+    ("sym_g64_hkv8", [999], 32, 8, 128, 0, 0, 64, 64),
 ]
 
 
@@ -161,6 +164,34 @@ def test_block_table_permutation_invariance():
     vp2 = {**vp, **{f: vp[f][inv] for f in ("data", "scales", "zeros")}}
     b = _run(q, kp2, vp2, perm[bt].astype(np.int32), seq_lens, 8, 128)
     torch.testing.assert_close(a, b, atol=0, rtol=0)
+
+
+def test_padded_head_layout_matches_dense():
+    """Heads padded apart within a token row take the per-head loader; dense
+    rows take the cooperative one.  Both meet the oracle tolerance and agree
+    with each other to an fp16 ulp or so (the compiler may contract the two
+    instantiations' float expressions differently)."""
+    seq_lens = [2000, 77]
+    hq, hkv, d = 32, 8, 128
+    bt, kp, vp = _build(seq_lens, hq, hkv, d, 1, 1, 32, 32, 81)
+    q = _query(2, hq, d, 81)
+    dense = _run(q, kp, vp, bt, seq_lens, hkv, d)
+    _check(dense, q, kp, vp, bt, seq_lens)
+
+    def padded(t, extra):
+        big = torch.zeros(t.shape[:-1] + (t.shape[-1] + extra,), dtype=t.dtype, device=DEV)
+        big[..., :t.shape[-1]] = t
+        return big[..., :t.shape[-1]]
+
+    kd, ks, kz = (padded(t, e) for t, e in zip(kvgen.plane_to_torch(kp, DEV), (16, 4, 4)))
+    vd, vs, vz = (padded(t, e) for t, e in zip(kvgen.plane_to_torch(vp, DEV), (16, 4, 4)))
+    assert kd.stride(2) == d // 2 + 16
+    out = K.fused_int4_decode(q.to(DEV), kd, vd, ks, vs, torch.from_numpy(bt).to(DEV),
+                              torch.tensor(seq_lens, dtype=torch.int32, device=DEV), hkv, d,
+                              k_zeros=kz, v_zeros=vz, asymmetric=True, group_size=32)
+    torch.cuda.synchronize()
+    _check(out, q, kp, vp, bt, seq_lens)
+    torch.testing.assert_close(out, dense, atol=2e-4, rtol=2.0 ** -9)
 
 
 def test_gqa_heads_equal_per_head_runs():
