@@ -40,6 +40,8 @@
 // Online softmax: a row's running max is raised only when a tile's max
 // exceeds it by more than 2 (log2 units).  Then p <= 4 and |P'| <= 4 * s_v,
 // which stays inside fp16 range for any finite fp16 K/V input (s_v < 9400).
+#include <cstdlib>
+
 #include "kv_decode.h"
 
 namespace knlp {
@@ -88,26 +90,17 @@ __device__ __forceinline__ float row_sum16(float x) {
   return x;
 }
 
-// 8 nibbles (one dword, element 2i in the low nibble of byte i) -> 8 exact
-// fp16 values 16 + n in slot order kNibK.  fp16 0x4C00 is 16.0; the nibble
-// goes to mantissa bits 6..9.
-// The mask and the 16.0 pattern are kept in VGPRs (see vgpr_const) so that
-// each output is one shift plus one v_and_or_b32: a gfx9 VOP3 instruction
-// cannot take two literal constants.
-__device__ __forceinline__ h8 nibbles_to_h8_b16(uint32_t w, uint32_t m, uint32_t c) {
+// 8 nibbles (one dword, element 2i in the low nibble of byte i) -> 8 fp16
+// values in slot order kNibK whose bit patterns are the nibbles themselves:
+// the exact subnormals n * 2^-24.  Seven VALU ops per dword.
+__device__ __forceinline__ h8 nibbles_to_h8_sub(uint32_t w) {
+  constexpr uint32_t m = 0x000F000Fu;
   u4 o;
-  o[0] = ((w << 6) & m) | c;   // n0, n4
-  o[1] = ((w << 2) & m) | c;   // n1, n5
-  o[2] = ((w >> 2) & m) | c;   // n2, n6
-  o[3] = ((w >> 6) & m) | c;   // n3, n7
+  o[0] = w & m;           // n0, n4
+  o[1] = (w >> 4) & m;    // n1, n5
+  o[2] = (w >> 8) & m;    // n2, n6
+  o[3] = (w >> 12) & m;   // n3, n7
   return __builtin_bit_cast(h8, o);
-}
-
-// A constant materialised in a VGPR the compiler cannot fold away.
-__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
-  uint32_t r;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
-  return r;
 }
 
 // nibbles of one dword as 8 int8 slots: [n0 n2 n4 n6 | n1 n3 n5 n7]
@@ -223,77 +216,92 @@ __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane,
 }
 
 // Running state of one wave.
+//
+// Tiles normally take the fast path: scores, a per-lane test that no row's
+// tile max exceeds its running max by more than the threshold, then
+// accumulate.  A tile that would raise a max (or the partial last tile) takes
+// the general path: masked scores, raise_max, masked accumulate.  Both paths
+// do the same arithmetic on rows whose max does not move, so the result does
+// not depend on which path a tile took.
 template <int NCH, int NG, bool KASYM, bool VASYM>
 struct WaveState {
   static constexpr int GPL = 4 / NG;
   h8 aq[NCH];          // masked q, A operands of QK (row = col)
-  float qsum[4];       // sum of q over the group of rows 4blk..4blk+3
-  f4 cinit;            // QK accumulator start: cancels the 16 bias (and the -8 of sym K)
+  float qsum24[4];     // 2^-24 * sum of q over the group of rows 4blk..4blk+3
+  f4 cinit;            // QK accumulator start: 0, or -8 * qsum24 for symmetric K
   h4 eye;              // identity, B operand of the P' transpose
-  long vsel[2];        // 64 * selection, B operand of the V transpose
-  f4 acc[NCH][2];      // PV accumulators, rows (g, vg) x columns d
-  float m_run[GPL];    // running max per q head (unscaled score units)
+  long vsel[2];        // selection, B operand of the V transpose
+  f4 acc[NCH][2];      // PV accumulators (units of 2^-24), rows (g, vg) x columns d
+  float m_run[GPL];    // running max per q head (score units of 2^-24)
   float lsum[GPL];     // per-lane partial softmax sums
-  float zacc[4];       // per-lane sum_t p * (z - 16 s), rows 4blk + e
-  float sl2;           // softmax_scale * log2(e)
-  float thr;           // rescale threshold 2 / sl2 (unscaled units)
-  uint32_t nib_mask;   // 0x03C003C0 in a VGPR
-  uint32_t nib_bias;   // 0x4C004C00 (fp16 16.0 twice) in a VGPR
+  float zacc[4];       // per-lane zero-point term, rows 4blk + e
+  float sl2;           // softmax_scale * log2(e) * 2^24
+  float thr;           // rescale threshold 2 / sl2 (score units)
 
+  // Scores of the two sub-tiles in units of 2^-24:
+  //   sum_kg s[t,kg] * S[(g,kg),t] + z[t,kg] * qsum24[(g,kg)].
   template <bool MASK>
-  __device__ __forceinline__ void step(const SubTile<NCH, NG> (&st)[2], int tbase, int t_end,
-                                       int col) {
-    bool valid[2] = {true, true};
-    if constexpr (MASK) {
-      valid[0] = tbase + col < t_end;
-      valid[1] = tbase + 16 + col < t_end;
-    }
-    // ---- scores (unscaled): sum_kg s * sum(q.n) + z * sum(q) ----------------
-    float score[2][GPL];
+  __device__ __forceinline__ void scores(const SubTile<NCH, NG> (&st)[2], const bool (&valid)[2],
+                                         float (&score)[2][GPL]) const {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       f4 S = cinit;
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            aq[c], nibbles_to_h8_b16(st[x].k.dw(c), nib_mask, nib_bias), S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[c], nibbles_to_h8_sub(st[x].k.dw(c)), S,
+                                                   0, 0, 0);
 #pragma unroll
       for (int gi = 0; gi < GPL; ++gi) {
         float sc = 0.0f;
 #pragma unroll
         for (int kg = 0; kg < NG; ++kg) {
           const int i = gi * NG + kg;
-          if constexpr (KASYM) sc = fmaf(st[x].kz.get(kg), qsum[i], sc);
+          if constexpr (KASYM) sc = fmaf(st[x].kz.get(kg), qsum24[i], sc);
           sc = fmaf(st[x].ks.get(kg), S[i], sc);
         }
         score[x][gi] = (MASK && !valid[x]) ? -INFINITY : sc;
       }
     }
-    // ---- lazy online-softmax max --------------------------------------------
+  }
+
+  // Does any row's tile max exceed its running max by more than thr?  No
+  // cross-lane reduction: a lane-wise test and a ballot.
+  __device__ __forceinline__ bool max_moves(const float (&score)[2][GPL]) const {
+    bool up = false;
+#pragma unroll
+    for (int gi = 0; gi < GPL; ++gi) up |= fmaxf(score[0][gi], score[1][gi]) > m_run[gi] + thr;
+    return __any(up);
+  }
+
+  // Raise the running max of the rows whose tile max exceeds it by more than
+  // thr, and rescale their accumulators.
+  __device__ __forceinline__ void raise_max(const float (&score)[2][GPL]) {
     float alpha[GPL];
-    bool need = false;
 #pragma unroll
     for (int gi = 0; gi < GPL; ++gi) {
       const float tmax = row_max16(fmaxf(score[0][gi], score[1][gi]));
       const bool up = tmax > m_run[gi] + thr;
       alpha[gi] = up ? __builtin_amdgcn_exp2f((m_run[gi] - tmax) * sl2) : 1.0f;
       m_run[gi] = up ? tmax : m_run[gi];
-      need |= up;
     }
-    if (__any(need)) {
 #pragma unroll
-      for (int gi = 0; gi < GPL; ++gi) lsum[gi] *= alpha[gi];
+    for (int gi = 0; gi < GPL; ++gi) lsum[gi] *= alpha[gi];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) zacc[e] *= alpha[e / NG];
+    for (int e = 0; e < 4; ++e) zacc[e] *= alpha[e / NG];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c)
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[c][h][i] *= alpha[i / NG];
-    }
-    // ---- P' = p * s_v (fp16 hi + lo), zero term, P' transpose ---------------
-    h8 ahi, alo;
+        for (int i = 0; i < 4; ++i) acc[c][h][i] *= alpha[i / NG];
+  }
+
+  // Probabilities p, P' = p * s_v split into fp16 hi + lo and transposed to
+  // the PV A operand (lane = row (g, vg), slots = tokens), and the
+  // zero-point term, for the two sub-tiles.
+  template <bool MASK>
+  __device__ __forceinline__ void probs(const SubTile<NCH, NG> (&st)[2], const bool (&valid)[2],
+                                        const float (&score)[2][GPL], h8& ahi, h8& alo) {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       float p[GPL];
@@ -303,23 +311,30 @@ struct WaveState {
         p[gi] = __builtin_amdgcn_exp2f((score[x][gi] - m_run[gi]) * sl2);   // 0 when masked
         lsum[gi] += p[gi];
       }
-      h4 xhi, xlo;
+      float sv[4], P[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int vg = e % NG;
-        float sv = st[x].vs.get(vg);
-        float zv = VASYM ? st[x].vz.get(vg) : -8.0f * sv;
-        if constexpr (MASK) {       // garbage scales past the end must not reach NaN
-          sv = valid[x] ? sv : 0.0f;
-          zv = valid[x] ? zv : 0.0f;
+        sv[e] = st[x].vs.get(e % NG);
+        if constexpr (MASK) sv[e] = valid[x] ? sv[e] : 0.0f;   // garbage past the end
+        P[e] = p[e / NG] * sv[e];
+        if constexpr (VASYM) {
+          float zv = st[x].vz.get(e % NG);
+          if constexpr (MASK) zv = valid[x] ? zv : 0.0f;
+          zacc[e] = fmaf(p[e / NG], zv, zacc[e]);
+        } else {
+          zacc[e] = fmaf(-8.0f, P[e], zacc[e]);          // symmetric: zero = -8 s
         }
-        const float pe = p[e / NG];
-        const float P = pe * sv;
-        const _Float16 hi = static_cast<_Float16>(P);
-        xhi[e] = hi;
-        xlo[e] = static_cast<_Float16>(fmaf(pe, sv, -static_cast<float>(hi)));
-        zacc[e] = fmaf(pe, fmaf(-16.0f, sv, zv), zacc[e]);
       }
+      const h2 hi01 = {static_cast<_Float16>(P[0]), static_cast<_Float16>(P[1])};
+      const h2 hi23 = {static_cast<_Float16>(P[2]), static_cast<_Float16>(P[3])};
+      const float r0 = fmaf(p[0 / NG], sv[0], -static_cast<float>(hi01[0]));
+      const float r1 = fmaf(p[1 / NG], sv[1], -static_cast<float>(hi01[1]));
+      const float r2 = fmaf(p[2 / NG], sv[2], -static_cast<float>(hi23[0]));
+      const float r3 = fmaf(p[3 / NG], sv[3], -static_cast<float>(hi23[1]));
+      const h2 lo01 = {static_cast<_Float16>(r0), static_cast<_Float16>(r1)};
+      const h2 lo23 = {static_cast<_Float16>(r2), static_cast<_Float16>(r3)};
+      const h4 xhi = {hi01[0], hi01[1], hi23[0], hi23[1]};
+      const h4 xlo = {lo01[0], lo01[1], lo23[0], lo23[1]};
       const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
       const f4 thi = __builtin_amdgcn_mfma_f32_16x16x16f16(xhi, eye, zero4, 0, 0, 0);
       const f4 tlo = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo, eye, zero4, 0, 0, 0);
@@ -332,16 +347,21 @@ struct WaveState {
       alo[4 * x + 0] = l01[0]; alo[4 * x + 1] = l01[1];
       alo[4 * x + 2] = l23[0]; alo[4 * x + 3] = l23[1];
     }
-    // ---- V transposes and PV ------------------------------------------------
-    const i4 vinit = {0x4C00, 0x4C00, 0x4C00, 0x4C00};
+  }
+
+  // PV with V transposed on the matrix cores (V arrives as lane = token):
+  // accumulator (c, h) holds column d = (D/4)(col/4) + 8c + 2(col%4) + h.
+  __device__ __forceinline__ void pv_transposed(const SubTile<NCH, NG> (&st)[2], const h8& ahi,
+                                                const h8& alo) {
+    const i4 vzero = {0, 0, 0, 0};
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const long va = nibbles_to_i8x8(st[0].v.dw(c));
       const long vb = nibbles_to_i8x8(st[1].v.dw(c));
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const i4 ta = __builtin_amdgcn_mfma_i32_16x16x32_i8(va, vsel[h], vinit, 0, 0, 0);
-        const i4 tb = __builtin_amdgcn_mfma_i32_16x16x32_i8(vb, vsel[h], vinit, 0, 0, 0);
+        const i4 ta = __builtin_amdgcn_mfma_i32_16x16x32_i8(va, vsel[h], vzero, 0, 0, 0);
+        const i4 tb = __builtin_amdgcn_mfma_i32_16x16x32_i8(vb, vsel[h], vzero, 0, 0, 0);
         u4 bw;
         bw[0] = static_cast<uint32_t>(ta[0]) | (static_cast<uint32_t>(ta[1]) << 16);
         bw[1] = static_cast<uint32_t>(ta[2]) | (static_cast<uint32_t>(ta[3]) << 16);
@@ -352,6 +372,86 @@ struct WaveState {
         acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
       }
     }
+  }
+
+  // PV with V read from LDS as lane = column: vw[x][i] holds the D/16 nibbles
+  // of columns (D/16)*col .. (D/16)*col + D/16 - 1 of token 16x + 4blk + i,
+  // the tokens of this lane's A slots 4x + i.  Accumulator j = 2c + h holds
+  // column d = (D/16) * col + j.  Token pairs are interleaved by halves with
+  // v_perm, then each column's nibble pair is one shift and one mask: the
+  // fp16 subnormal bit patterns of slots (2q, 2q + 1).
+  __device__ __forceinline__ void pv_columns(const uint32_t (&vw)[2][4], const h8& ahi,
+                                             const h8& alo) {
+    uint32_t u0[4], u1[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a = vw[q / 2][2 * (q % 2)];
+      const uint32_t b = vw[q / 2][2 * (q % 2) + 1];
+      u0[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);   // a.lo16 | b.lo16 << 16
+      u1[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);   // a.hi16 | b.hi16 << 16
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * c + h;
+        u4 bw;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bw[q] = ((j < 4 ? u0[q] : u1[q]) >> (4 * (j % 4))) & 0x000F000Fu;
+        const h8 bv = __builtin_bit_cast(h8, bw);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
+      }
+    }
+  }
+
+  template <bool MASK>
+  __device__ __forceinline__ void accumulate(const SubTile<NCH, NG> (&st)[2],
+                                             const bool (&valid)[2],
+                                             const float (&score)[2][GPL]) {
+    h8 ahi, alo;
+    probs<MASK>(st, valid, score, ahi, alo);
+    pv_transposed(st, ahi, alo);
+  }
+
+  template <bool MASK>
+  __device__ __forceinline__ void accumulate_cols(const SubTile<NCH, NG> (&st)[2],
+                                                  const uint32_t (&vw)[2][4],
+                                                  const bool (&valid)[2],
+                                                  const float (&score)[2][GPL]) {
+    h8 ahi, alo;
+    probs<MASK>(st, valid, score, ahi, alo);
+    pv_columns(vw, ahi, alo);
+  }
+
+  // General step: any tile, masked or not, max moving or not.
+  template <bool MASK>
+  __device__ __forceinline__ void step(const SubTile<NCH, NG> (&st)[2], int tbase, int t_end,
+                                       int col) {
+    bool valid[2] = {true, true};
+    if constexpr (MASK) {
+      valid[0] = tbase + col < t_end;
+      valid[1] = tbase + 16 + col < t_end;
+    }
+    float score[2][GPL];
+    scores<MASK>(st, valid, score);
+    if (max_moves(score)) raise_max(score);
+    accumulate<MASK>(st, valid, score);
+  }
+
+  template <bool MASK>
+  __device__ __forceinline__ void step_cols(const SubTile<NCH, NG> (&st)[2],
+                                            const uint32_t (&vw)[2][4], int tbase, int t_end,
+                                            int col) {
+    bool valid[2] = {true, true};
+    if constexpr (MASK) {
+      valid[0] = tbase + col < t_end;
+      valid[1] = tbase + 16 + col < t_end;
+    }
+    float score[2][GPL];
+    scores<MASK>(st, valid, score);
+    if (max_moves(score)) raise_max(score);
+    accumulate_cols<MASK>(st, vw, valid, score);
   }
 };
 
@@ -397,14 +497,15 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W
   qpart += __shfl_xor(qpart, 32, kWave);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    W.qsum[i] = __shfl(qpart, 4 * blk + i, kWave);
-    W.cinit[i] = (KASYM ? -16.0f : -24.0f) * W.qsum[i];
+    // 2^-24 is exact in fp32: K codes enter the QK product as n * 2^-24
+    W.qsum24[i] = __shfl(qpart, 4 * blk + i, kWave) * 0x1p-24f;
+    W.cinit[i] = KASYM ? 0.0f : -8.0f * W.qsum24[i];
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.eye[e] = (blk == col / 4 && e == col % 4) ? 1.0f : 0.0f;
 #pragma unroll
   for (int h = 0; h < 2; ++h)
-    W.vsel[h] = blk == col / 4 ? static_cast<long>(64ull << (8 * (4 * h + col % 4))) : 0l;
+    W.vsel[h] = blk == col / 4 ? static_cast<long>(1ull << (8 * (4 * h + col % 4))) : 0l;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) W.acc[c][0] = W.acc[c][1] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -414,14 +515,13 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.zacc[e] = 0.0f;
-  W.sl2 = a.scale_log2;
-  W.thr = kRescaleLog2 / a.scale_log2;
-  W.nib_mask = vgpr_const(0x03C003C0u);
-  W.nib_bias = vgpr_const(0x4C004C00u);
+  W.sl2 = a.scale_log2 * 0x1p24f;      // scores are in units of 2^-24
+  W.thr = kRescaleLog2 / W.sl2;
 }
 
-// Reduce over tokens and write the wave's partial (acc, max, sum).
-template <int D, int NG, bool KASYM, bool VASYM>
+// Reduce over tokens and write the wave's partial (acc, max, sum).  COLS:
+// the accumulators follow pv_columns' column order, else pv_transposed's.
+template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false>
 __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM>& W,
                                                const DecodeArgs& a, int seq, int kvh,
                                                int split, int col, int blk) {
@@ -438,14 +538,15 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
   for (int c = 0; c < NCH; ++c) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int d = (D / 4) * (col / 4) + 8 * c + 2 * (col % 4) + h;
+      const int d = COLS ? (D / 16) * col + 2 * c + h
+                         : (D / 4) * (col / 4) + 8 * c + 2 * (col % 4) + h;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * blk + i;
         const int g = r / NG;
         if (g < G && d / gs == r % NG) {
           const int64_t row = (row0 + g) * a.num_splits + split;
-          a.part_o[row * D + d] = W.acc[c][h][i] + W.zacc[i];
+          a.part_o[row * D + d] = fmaf(W.acc[c][h][i], 0x1p24f, W.zacc[i]);
         }
       }
     }
@@ -553,94 +654,137 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
 //
 // A block is 8 waves serving 8 consecutive kv heads of one (sequence, split),
 // so each 16-token sub-tile of each array (codes K and V, scales and zeros) is
-// 16 rows of 8 heads' contiguous bytes.  All 512 threads fetch a 32-token tile
-// with 16-byte loads (one wave instruction = 1 KB of consecutive rows), one
-// tile ahead in registers, then store it to LDS with padded rows; after a
-// barrier each wave reads its own head's slice in the lane layout of the
-// per-head kernel.  Per-head loads touch 64-byte fragments at a 512-byte
-// stride and 8-byte scale fragments at a 64-byte stride, which measured
-// 55-59% of HBM peak even without compute; page-contiguous loads measured
-// 82-85%, as fast as a plain stream.
+// 16 rows of 8 heads' contiguous bytes.  The block copies a 32-token tile
+// from HBM straight into LDS with buffer_load ... lds (16 bytes per lane, one
+// wave instruction = 1 KB of consecutive rows), one tile ahead of the
+// compute; after a barrier each wave reads its own head's slice in the lane
+// layout of the per-head kernel.  Per-head loads touch 64-byte fragments at a
+// 512-byte stride and 8-byte scale fragments at a 64-byte stride, which
+// measured 55-59% of HBM peak even without compute; page-contiguous loads
+// measured 82-85%, as fast as a plain stream.  The direct-to-LDS copy keeps
+// the staging out of VGPRs, so two blocks (16 waves) fit on a CU.
 // ---------------------------------------------------------------------------
 template <int D, int NG>
 struct CoopLayout {
   static constexpr int kHeads = 8;
   static constexpr int HB = D / 2;                // code bytes per head and token
   static constexpr int SB = 2 * NG;               // scale bytes per head and token
-  static constexpr int CPR = kHeads * HB / 16;    // 16-byte chunks per code row
-  static constexpr int NCC = 16 * CPR;            // code chunks per sub-tile
-  static constexpr int CROW = kHeads * HB + 16;   // padded LDS row of codes
-  static constexpr int SROW = kHeads * SB + 8;    // padded LDS row of one scale array
+  static constexpr int CROW = kHeads * HB;        // LDS row of codes (16 rows per sub-tile)
+  static constexpr int SROW = kHeads * SB;        // LDS row of one scale array
+  static constexpr int CPS = 16 * CROW / 1024;    // 1-KB wave copies per code sub-tile
+  static constexpr int NJ = 2 * 2 * CPS / 8;      // code copies per wave and tile
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = 2 * 16 * CROW;
   static constexpr int S_OFF = 4 * 16 * CROW;     // 4 arrays (ks, vs, kz, vz) x 2 sub-tiles
   static constexpr int BYTES = S_OFF + 8 * 16 * SROW;
-  static_assert(NCC <= 512, "one code chunk per thread and sub-tile");
-  static_assert(16 * NG <= kWave, "one scale chunk per lane");
+  static_assert(8 % CPS == 0 && NJ >= 1, "code sub-tiles split evenly over the 8 waves");
+  static_assert(16 * SROW <= 1024, "one wave copy per scale sub-tile");
+  // Rows are not padded; bank conflicts are avoided by XOR swizzles, so two
+  // blocks' double buffers fit one CU's LDS.  The 16-byte chunk c of code
+  // row r (r < 16) lives at chunk c ^ r: the 16 rows a wave reads at one head
+  // offset then cover all 64 banks.
+  __host__ __device__ static constexpr int code_off(int r, int byte) {
+    return r * CROW + ((((byte >> 4) ^ r) << 4) | (byte & 15));
+  }
+  // The 16-byte chunk c of scale row r lives at chunk c ^ scale_swz(r); the
+  // 16 rows' slots of one head then fall in distinct banks.
+  __host__ __device__ static constexpr int scale_swz(int r) {
+    return SROW >= 32 ? (r * SROW / 256) & (SROW / 16 - 1) : 0;
+  }
+  __host__ __device__ static constexpr int scale_off(int r, int byte) {
+    return r * SROW + ((((byte >> 4) ^ scale_swz(r)) << 4) | (byte & 15));
+  }
 };
 
-// One thread's share of a 32-token tile, in flight between HBM and LDS.
-struct CoopStage {
-  uint4 k[2], v[2];   // code chunk of sub-tile 0 and 1
-  uint4 s;            // scale chunk (array and sub-tile fixed per wave)
-};
-
-// Loop-invariant addressing of the cooperative loader.
+// Loop-invariant addressing of the cooperative copy.
 struct CoopAddr {
   const uint8_t* kc;      // codes of head h0 (block/page strides below)
   const uint8_t* vc;
   const uint8_t* sp;      // this wave's scale array, head h0
   int64_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
-  uint32_t lk, lv, ls;    // lane byte offsets
-  int lds_c, lds_s;       // LDS byte offsets of this thread's chunks
-  bool c_on, s_on;
-  int s_x;                // sub-tile whose scale chunk this wave loads
+  uint32_t lk, lv, ls;    // lane byte offsets in HBM
+  bool s_arr_on;          // this wave copies a scale array (wave-uniform)
+  bool s_on;              // this lane copies a scale chunk
+  int s_x;                // sub-tile whose scale chunk this wave copies
+  int s_lds;              // LDS offset of this wave's scale sub-tile
   const int32_t* bt;
   int bs_shift;
 };
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+typedef const __attribute__((address_space(4))) int32_t* bt_scalar_t;
+
+// 16 bytes per lane from a raw buffer straight into LDS at m0 + 16 * lane.
+// Written as inline asm so that the compiler does not track these copies:
+// its conservative tracking would put a full vector-memory wait before
+// every LDS read, serialising the copies of later tiles with the compute of
+// this one.  All waits for the copies are explicit (wait_vmcnt) and
+// followed by a block barrier before any wave reads the copied bytes.
+__device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, const void* lds_dst) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const i4 rsrc = {static_cast<int>(b), static_cast<int>((b >> 32) & 0xFFFF), -1, 0x00020000};
+  const uint32_t m0 = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(lds_dst)));
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(m0)
+               : "memory", "m0");
+}
+
+// Issue the copies of the 32-token tile at `tb` into `buf` (this wave's part).
+// Page numbers come through the scalar cache (s_load), so looking one up
+// never waits on the vector-memory counter that tracks the copies in flight.
 template <int D, int NG>
-__device__ __forceinline__ void coop_load(const CoopAddr& C, PageWindow& P, int lane, int tb,
-                                          int t_end, CoopStage& R) {
+__device__ __forceinline__ void coop_issue(const CoopAddr& C, int wave, int tb, int t_end,
+                                           uint8_t* buf) {
+  using L = CoopLayout<D, NG>;
+  const bt_scalar_t bt = (bt_scalar_t)(C.bt);
   int64_t page[2], off[2];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     // a second half wholly past the end re-reads the first half's page (masked)
     const int pb = (x == 0 || tb + 16 < t_end) ? tb + 16 * x : tb;
-    page[x] = P.page(C.bt, lane, pb >> C.bs_shift);
+    page[x] = bt[pb >> C.bs_shift];
     off[x] = pb & ((1 << C.bs_shift) - 1);
   }
 #pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    if (CoopLayout<D, NG>::NCC == 512 || C.c_on) {
-      R.k[x] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-          rsrc_of(C.kc + (page[x] * C.kc_b + off[x] * C.kc_p)), C.lk, 0, 0));
-      R.v[x] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-          rsrc_of(C.vc + (page[x] * C.vc_b + off[x] * C.vc_p)), C.lv, 0, 0));
-    }
+  for (int j = 0; j < L::NJ; ++j) {
+    const int q = wave + 8 * j;                  // 1-KB copy index within the tile
+    const int arr = q / (2 * L::CPS);            // 0 = K, 1 = V
+    const int x = (q / L::CPS) & 1;
+    const int part = q % L::CPS;
+    const uint8_t* base = arr == 0 ? C.kc + (page[x] * C.kc_b + off[x] * C.kc_p)
+                                   : C.vc + (page[x] * C.vc_b + off[x] * C.vc_p);
+    uint8_t* dst = buf + (arr == 0 ? L::K_OFF : L::V_OFF) + x * 16 * L::CROW + part * 1024;
+    lds_copy16(base, arr == 0 ? C.lk : C.lv, dst);
   }
-  if (C.s_on) {
+  if (C.s_arr_on) {
     const int64_t pg = C.s_x ? page[1] : page[0];
     const int64_t of = C.s_x ? off[1] : off[0];
-    R.s = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-        rsrc_of(C.sp + (pg * C.sp_b + of * C.sp_p)), C.ls, 0, 0));
+    if (C.s_on) lds_copy16(C.sp + (pg * C.sp_b + of * C.sp_p), C.ls, buf + C.s_lds);
   }
 }
 
-template <int D, int NG>
-__device__ __forceinline__ void coop_store(const CoopAddr& C, uint8_t* buf, const CoopStage& R) {
-  using L = CoopLayout<D, NG>;
-  if (L::NCC == 512 || C.c_on) {
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      *reinterpret_cast<uint4*>(buf + L::K_OFF + x * 16 * L::CROW + C.lds_c) = R.k[x];
-      *reinterpret_cast<uint4*>(buf + L::V_OFF + x * 16 * L::CROW + C.lds_c) = R.v[x];
-    }
-  }
-  if (C.s_on) {
-    // padded scale rows are 8-byte aligned
-    *reinterpret_cast<uint2*>(buf + C.lds_s) = make_uint2(R.s.x, R.s.y);
-    *reinterpret_cast<uint2*>(buf + C.lds_s + 8) = make_uint2(R.s.z, R.s.w);
+// s_waitcnt for "at most N vector-memory operations outstanding" (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at max).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Wait until this wave's copies of the next tile have landed, leaving the
+// copies of `later` further tiles in flight (each tile is NJ copies, plus one
+// for the waves that copy a scale array).
+template <int NJ>
+__device__ __forceinline__ void wait_tile_copies(int later, bool scale_wave) {
+  if (later <= 0) {
+    wait_vmcnt<0>();
+  } else if (later == 1) {
+    if (scale_wave) wait_vmcnt<NJ + 1>(); else wait_vmcnt<NJ>();
+  } else {
+    if (scale_wave) wait_vmcnt<2 * (NJ + 1)>(); else wait_vmcnt<2 * NJ>();
   }
 }
 
@@ -654,6 +798,7 @@ __device__ __forceinline__ void halves_from_lds(Halves<NG>& h, const uint8_t* p)
     h.v = *reinterpret_cast<const uint16_t*>(p);
 }
 
+// This wave's head slice of the tile in `buf`, in the per-head lane layout.
 template <int D, int NG, bool KASYM, bool VASYM>
 __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col, int blk,
                                           SubTile<D / 32, NG> (&st)[2]) {
@@ -661,15 +806,12 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
   constexpr int LB = D / 8;
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    const int co = x * 16 * L::CROW + col * L::CROW + wave * L::HB + blk * LB;
-    if constexpr (D == 128) {
+    const int co = x * 16 * L::CROW + L::code_off(col, wave * L::HB + blk * LB);
+    if constexpr (D == 128)
       st[x].k.v = *reinterpret_cast<const uint4*>(buf + L::K_OFF + co);
-      st[x].v.v = *reinterpret_cast<const uint4*>(buf + L::V_OFF + co);
-    } else {
+    else
       st[x].k.v = *reinterpret_cast<const uint2*>(buf + L::K_OFF + co);
-      st[x].v.v = *reinterpret_cast<const uint2*>(buf + L::V_OFF + co);
-    }
-    const int so = L::S_OFF + x * 16 * L::SROW + col * L::SROW + wave * L::SB;
+    const int so = L::S_OFF + x * 16 * L::SROW + L::scale_off(col, wave * L::SB);
     halves_from_lds<NG>(st[x].ks, buf + so);
     halves_from_lds<NG>(st[x].vs, buf + so + 1 * 2 * 16 * L::SROW);
     if constexpr (KASYM) halves_from_lds<NG>(st[x].kz, buf + so + 2 * 2 * 16 * L::SROW);
@@ -677,11 +819,75 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
   }
 }
 
-template <int D, int NG, bool KASYM, bool VASYM>
-__global__ __launch_bounds__(512) void decode_mfma_coop_kernel(DecodeArgs a) {
+// V of this wave's head as PV B operands (pv_columns): vw[x][i] holds the
+// D/32 bytes at columns (D/16)*col.. of token 16x + 4blk + i.  The four lane
+// blocks read rows 4blk + i, whose chunk swizzles differ, so the 64 lanes
+// hit 64 distinct banks.
+template <int D, int NG>
+__device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int col, int blk,
+                                            uint32_t (&vw)[2][4]) {
+  using L = CoopLayout<D, NG>;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int o = L::V_OFF + x * 16 * L::CROW +
+                    L::code_off(4 * blk + i, wave * L::HB + (D / 32) * col);
+      if constexpr (D == 128)
+        vw[x][i] = *reinterpret_cast<const uint32_t*>(buf + o);
+      else
+        vw[x][i] = *reinterpret_cast<const uint16_t*>(buf + o);
+    }
+}
+
+// One tile, software-pipelined with the previous one: read this wave's slice
+// of tile i from `cur`, start the copy of tile i + NBUF - 1 into `nxt` (the
+// buffer tile i - 1 used), then QK and scores of tile i next to PV of tile
+// i - 1 (independent work for the matrix cores while the VALU converts and
+// scales), the running-max update, and P' of tile i, which PV consumes in
+// the next call.  Ends with a wait for this wave's copies of tile i + 1 and
+// a block barrier, after which every wave's copies of tile i + 1 have landed.
+template <int D, int NG, bool KASYM, bool VASYM, int NBUF, bool MASK, bool PV_PREV>
+__device__ __forceinline__ void coop_tile(WaveState<D / 32, NG, KASYM, VASYM>& W,
+                                          const CoopAddr& C, int i, int ntiles, int t_begin,
+                                          int t_end, int wave, int col, int blk,
+                                          const uint8_t* cur, uint8_t* nxt, uint32_t (&vw)[2][4],
+                                          h8& ahi, h8& alo) {
+  constexpr int NCH = D / 32;
+  const int tb = t_begin + 32 * i;
+  SubTile<NCH, NG> st[2];
+  uint32_t vn[2][4];
+  coop_read<D, NG, KASYM, VASYM>(cur, wave, col, blk, st);
+  coop_read_v<D, NG>(cur, wave, col, blk, vn);
+  if (i + NBUF - 1 < ntiles) coop_issue<D, NG>(C, wave, tb + 32 * (NBUF - 1), t_end, nxt);
+  bool valid[2] = {true, true};
+  if constexpr (MASK) {
+    valid[0] = tb + col < t_end;
+    valid[1] = tb + 16 + col < t_end;
+  }
+  float score[2][4 / NG];
+  W.template scores<MASK>(st, valid, score);
+  if constexpr (PV_PREV) W.pv_columns(vw, ahi, alo);
+  if (W.max_moves(score)) W.raise_max(score);
+  W.template probs<MASK>(st, valid, score, ahi, alo);
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) vw[x][k] = vn[x][k];
+  // copies issued after tile i + 1's: tiles i + 2 .. min(i + NBUF - 1, ntiles - 1)
+  wait_tile_copies<CoopLayout<D, NG>::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
+  __syncthreads();
+}
+
+// One block per CU (8 waves), NBUF tile buffers of LDS: the copies run
+// NBUF - 1 tiles ahead of the compute.
+template <int D, int NG, bool KASYM, bool VASYM, int NBUF>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(NBUF == 2 ? 4 : 2)))
+void decode_mfma_coop_kernel(DecodeArgs a) {
   using L = CoopLayout<D, NG>;
   constexpr int NCH = D / 32;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][L::BYTES];
+  static_assert(NBUF >= 2 && NBUF <= 4, "copies one to three tiles ahead");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][L::BYTES];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int col = lane & 15;
@@ -708,13 +914,16 @@ __global__ __launch_bounds__(512) void decode_mfma_coop_kernel(DecodeArgs a) {
     C.vc = static_cast<const uint8_t*>(V.data) + h0 * V.stride_head;
     C.kc_b = K.stride_block; C.kc_p = K.stride_page;
     C.vc_b = V.stride_block; C.vc_p = V.stride_page;
-    const int c_row = tid / L::CPR;
-    const int c_byte = 16 * (tid % L::CPR);
-    C.c_on = tid < L::NCC;
-    C.lk = static_cast<uint32_t>(c_row * K.stride_page + c_byte);
-    C.lv = static_cast<uint32_t>(c_row * V.stride_page + c_byte);
-    C.lds_c = c_row * L::CROW + c_byte;
-    // wave w loads scale array w / 2 (ks, vs, kz, vz) of sub-tile w % 2
+    // code copy: lane -> LDS byte part*1024 + 16*lane of a sub-tile, which
+    // holds logical chunk (physical chunk) ^ row of that row
+    {
+      const int byte = (wave % L::CPS) * 1024 + 16 * lane;
+      const int r = byte / L::CROW;
+      const int c = ((byte % L::CROW) >> 4) ^ r;
+      C.lk = static_cast<uint32_t>(r * K.stride_page + 16 * c);
+      C.lv = static_cast<uint32_t>(r * V.stride_page + 16 * c);
+    }
+    // wave w copies scale array w / 2 (ks, vs, kz, vz) of sub-tile w % 2
     const int arr = wave >> 1;
     C.s_x = wave & 1;
     const uint16_t* base = arr == 0 ? static_cast<const uint16_t*>(K.scales)
@@ -728,46 +937,48 @@ __global__ __launch_bounds__(512) void decode_mfma_coop_kernel(DecodeArgs a) {
     const int64_t spg = arr == 0 ? K.s_stride_page : arr == 1 ? V.s_stride_page
                       : arr == 2 ? K.z_stride_page : V.z_stride_page;
     const bool arr_on = arr < 2 || (arr == 2 && KASYM) || (arr == 3 && VASYM);
-    C.s_on = arr_on && lane < 16 * NG;
+    C.s_arr_on = arr_on;
+    C.s_on = arr_on && 16 * lane < 16 * L::SROW;
     C.sp = arr_on ? reinterpret_cast<const uint8_t*>(base + h0 * sh) : nullptr;
     C.sp_b = 2 * sbk;
     C.sp_p = 2 * spg;
-    const int s_row = lane / NG;
-    const int s_byte = 16 * (lane % NG);
-    C.ls = static_cast<uint32_t>(s_row * C.sp_p + s_byte);
-    C.lds_s = L::S_OFF + (arr * 2 + C.s_x) * 16 * L::SROW + s_row * L::SROW + s_byte;
+    {
+      const int byte = 16 * lane;
+      const int r = byte / L::SROW;
+      const int c = ((byte % L::SROW) >> 4) ^ L::scale_swz(r);
+      C.ls = static_cast<uint32_t>(r * C.sp_p + 16 * c);
+    }
+    C.s_lds = L::S_OFF + (arr * 2 + C.s_x) * 16 * L::SROW;
     C.bt = a.block_table + seq * a.bt_stride;
     C.bs_shift = a.block_shift;
   }
 
-  PageWindow PW;
-  PW.last = (t_end - 1) >> C.bs_shift;
-  PW.fill(C.bt, lane, t_begin >> C.bs_shift);
-
-  // Tile i computes from LDS buffer i % 2 while tile i + 1 is in flight in
-  // registers; after the compute it goes to the other buffer and tile i + 2
-  // is requested.  One barrier per tile.
   const int ntiles = (t_end - t_begin + 31) / 32;
-  CoopStage R;
-  coop_load<D, NG>(C, PW, lane, t_begin, t_end, R);
-  coop_store<D, NG>(C, lds[0], R);
-  if (ntiles > 1) coop_load<D, NG>(C, PW, lane, t_begin + 32, t_end, R);
+#pragma unroll
+  for (int t = 0; t < NBUF - 1; ++t)
+    if (t < ntiles) coop_issue<D, NG>(C, wave, t_begin + 32 * t, t_end, lds[t]);
+  wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
   __syncthreads();
-  for (int i = 0; i < ntiles; ++i) {
-    const int tb = t_begin + 32 * i;
-    SubTile<NCH, NG> st[2];
-    coop_read<D, NG, KASYM, VASYM>(lds[i & 1], wave, col, blk, st);
-    if (tb + 32 <= t_end)
-      W.template step<false>(st, tb, t_end, col);
-    else
-      W.template step<true>(st, tb, t_end, col);
-    if (i + 1 < ntiles) {
-      coop_store<D, NG>(C, lds[(i + 1) & 1], R);
-      if (i + 2 < ntiles) coop_load<D, NG>(C, PW, lane, tb + 64, t_end, R);
-    }
-    __syncthreads();
+  // tile 0 (no PV pending), full tiles, an optional partial last tile, and
+  // the PV of the last tile
+  uint32_t vw[2][4];
+  h8 ahi, alo;
+  const int nfull = (t_end - t_begin) / 32;
+#define KNLP_COOP_TILE(MASK, PV_PREV)                                                     \
+  coop_tile<D, NG, KASYM, VASYM, NBUF, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, \
+                                                      col, blk, lds[i % NBUF],            \
+                                                      lds[(i + NBUF - 1) % NBUF], vw, ahi, alo)
+  int i = 0;
+  if (nfull > 0) {
+    KNLP_COOP_TILE(false, false);
+    for (i = 1; i < nfull; ++i) KNLP_COOP_TILE(false, true);
+    if (i < ntiles) KNLP_COOP_TILE(true, true);
+  } else {
+    KNLP_COOP_TILE(true, false);
   }
-  write_partials<D, NG, KASYM, VASYM>(W, a, seq, kvh, split, col, blk);
+#undef KNLP_COOP_TILE
+  W.pv_columns(vw, ahi, alo);
+  write_partials<D, NG, KASYM, VASYM, true>(W, a, seq, kvh, split, col, blk);
 }
 
 int heads_per_block_mfma(int num_kv_heads) {
@@ -815,21 +1026,30 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const bool coop = coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
                     coop_layout_ok(a.vp, head_size, a.num_kv_heads);
   const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
+  static const int nbuf = [] {
+    const char* e = getenv("KNLP_COOP_BUFFERS");
+    const int n = e ? atoi(e) : 3;
+    return n == 2 || n == 4 ? n : 3;
+  }();
   const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
   const dim3 block(kWave * hpb);
-#define KNLP_MFMA_K(KERNEL, D, NG)                                                       \
+#define KNLP_MFMA_K(KERNEL, D, NG, ...)                                                  \
   if (ka && va)                                                                          \
-    hipLaunchKernelGGL((KERNEL<D, NG, true, true>), grid, block, 0, stream, a);          \
+    hipLaunchKernelGGL((KERNEL<D, NG, true, true __VA_ARGS__>), grid, block, 0, stream, a);  \
   else if (ka)                                                                           \
-    hipLaunchKernelGGL((KERNEL<D, NG, true, false>), grid, block, 0, stream, a);         \
+    hipLaunchKernelGGL((KERNEL<D, NG, true, false __VA_ARGS__>), grid, block, 0, stream, a); \
   else if (va)                                                                           \
-    hipLaunchKernelGGL((KERNEL<D, NG, false, true>), grid, block, 0, stream, a);         \
+    hipLaunchKernelGGL((KERNEL<D, NG, false, true __VA_ARGS__>), grid, block, 0, stream, a); \
   else                                                                                   \
-    hipLaunchKernelGGL((KERNEL<D, NG, false, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((KERNEL<D, NG, false, false __VA_ARGS__>), grid, block, 0, stream, a);
 #define KNLP_MFMA(D, NG)                                                                 \
   if (head_size == D && ng == NG) {                                                      \
-    if (coop) {                                                                          \
-      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG)                                        \
+    if (coop && nbuf == 4) {                                                             \
+      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG, , 4)                                   \
+    } else if (coop && nbuf == 2) {                                                      \
+      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG, , 2)                                   \
+    } else if (coop) {                                                                   \
+      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG, , 3)                                   \
     } else {                                                                             \
       KNLP_MFMA_K(decode_mfma_kernel, D, NG)                                             \
     }                                                                                    \
