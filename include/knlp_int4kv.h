@@ -96,12 +96,15 @@ int knlp_kv_append(const void* key, const void* value, int32_t src_dtype,
 
 /*
  * Split-K plan: tokens per split for a batch whose longest possible context
- * is max_context (= block-table width * block_size; no device read-back).
- * Returns the split length in tokens (> 0) or a negative status.
+ * is max_context (= block-table width * block_size; no device read-back),
+ * for K/V planes of the given knlp_kv_format values (the kernel that will
+ * run decides how many workgroups a CU holds).  Returns the split length in
+ * tokens (> 0) or a negative status.
  */
 int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads,
                                     int32_t num_q_heads, int32_t head_size,
-                                    int32_t max_context);
+                                    int32_t max_context, int32_t k_format,
+                                    int32_t v_format);
 
 /* Bytes of fp32 workspace decode needs for this shape and split length. */
 int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,

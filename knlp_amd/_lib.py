@@ -57,7 +57,7 @@ _SIGS = {
     "knlp_status_string": (ctypes.c_char_p, [_I32]),
     "knlp_kv_append": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I64, _I64, _I64, _I64,
                               _PLANE, _PLANE, _P, _I32, _I32, _F, _P]),
-    "knlp_kv_decode_split_tokens": (_I32, [_I32, _I32, _I32, _I32, _I32]),
+    "knlp_kv_decode_split_tokens": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "knlp_kv_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
     "knlp_kv_decode_partial": (_I32, [_P, _I32, _I64, _I64, _I32, _I32, _I32, _I32,
                                       _PLANE, _PLANE, _P, _I64, _P, _I32, _I32, _F, _I32,

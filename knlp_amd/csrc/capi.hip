@@ -149,17 +149,22 @@ int knlp_kv_append(const void* key, const void* value, int32_t src_dtype, int64_
 }
 
 int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads, int32_t num_q_heads,
-                                    int32_t head_size, int32_t max_context) {
+                                    int32_t head_size, int32_t max_context, int32_t k_format,
+                                    int32_t v_format) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || max_context <= 0 || head_size <= 0)
     return KNLP_ERR_SHAPE;
   (void)num_q_heads;
-  // Aim for about two resident workgroups per CU over the whole batch, but
-  // never below 256 tokens per split (partials cost (D+2)*4 bytes per q head
-  // per split on each side of the merge) and always a multiple of 64 tokens.
-  const int64_t groups = static_cast<int64_t>(num_seqs) *
-                         ((num_kv_heads + heads_per_block(num_kv_heads) - 1) /
-                          heads_per_block(num_kv_heads));
-  const int64_t target = 2LL * num_cus();
+  // Aim for about two resident workgroups per CU over the whole batch (one
+  // for INT4 K/V with Hkv % 8 == 0: the matrix-core kernel then runs one
+  // 8-wave block per CU that holds 120-160 KB of LDS tile buffers), but never
+  // below 256 tokens per split (partials cost (D+2)*4 bytes per q head per
+  // split on each side of the merge) and always a multiple of 64 tokens.
+  const auto int4 = [](int f) { return f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM; };
+  const bool wide = num_kv_heads % 8 == 0 && int4(k_format) && int4(v_format);
+  const int hpb = wide ? 8 : heads_per_block(num_kv_heads);
+  const int64_t groups =
+      static_cast<int64_t>(num_seqs) * ((num_kv_heads + hpb - 1) / hpb);
+  const int64_t target = (wide ? 1LL : 2LL) * num_cus();
   int64_t splits = (target + groups - 1) / groups;
   if (splits < 1) splits = 1;
   int64_t tok = (max_context + splits - 1) / splits;

@@ -245,7 +245,7 @@ struct WaveState {
                                          float (&score)[2][GPL]) const {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-      f4 S = cinit;
+      f4 S = KASYM ? f4{0.f, 0.f, 0.f, 0.f} : cinit;
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
         S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[c], nibbles_to_h8_sub(st[x].k.dw(c)), S,
@@ -499,7 +499,7 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W
   for (int i = 0; i < 4; ++i) {
     // 2^-24 is exact in fp32: K codes enter the QK product as n * 2^-24
     W.qsum24[i] = __shfl(qpart, 4 * blk + i, kWave) * 0x1p-24f;
-    W.cinit[i] = KASYM ? 0.0f : -8.0f * W.qsum24[i];
+    if constexpr (!KASYM) W.cinit[i] = -8.0f * W.qsum24[i];
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.eye[e] = (blk == col / 4 && e == col % 4) ? 1.0f : 0.0f;
@@ -1028,8 +1028,8 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
   static const int nbuf = [] {
     const char* e = getenv("KNLP_COOP_BUFFERS");
-    const int n = e ? atoi(e) : 3;
-    return n == 2 || n == 4 ? n : 3;
+    const int n = e ? atoi(e) : 4;
+    return n == 2 || n == 3 ? n : 4;
   }();
   const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
   const dim3 block(kWave * hpb);

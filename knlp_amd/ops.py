@@ -176,7 +176,7 @@ def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, 
     max_context = block_table.shape[1] * block_size
     if split_tokens is None:
         split_tokens = config.DECODE_SPLIT_TOKENS or L.knlp_kv_decode_split_tokens(
-            num_seqs, num_kv_heads, num_heads, head_size, max_context)
+            num_seqs, num_kv_heads, num_heads, head_size, max_context, kp.format, vp.format)
         check(split_tokens, "knlp_kv_decode_split_tokens")
     ws_bytes = L.knlp_kv_decode_workspace_bytes(max(num_seqs, 1), num_heads, head_size,
                                                 max_context, split_tokens)

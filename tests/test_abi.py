@@ -37,9 +37,10 @@ def test_abi_version_and_status_strings():
 
 def test_split_plan_and_workspace():
     L = _lib.lib()
-    st = L.knlp_kv_decode_split_tokens(8, 8, 32, 128, 32768)
+    a4 = _lib.KV_INT4_ASYM
+    st = L.knlp_kv_decode_split_tokens(8, 8, 32, 128, 32768, a4, a4)
     assert st > 0 and st % 64 == 0
-    assert L.knlp_kv_decode_split_tokens(0, 8, 32, 128, 32768) == _lib.ERR_SHAPE
+    assert L.knlp_kv_decode_split_tokens(0, 8, 32, 128, 32768, a4, a4) == _lib.ERR_SHAPE
     ws = L.knlp_kv_decode_workspace_bytes(8, 32, 128, 32768, st)
     ns = -(-32768 // st)
     assert ws == 8 * 32 * ns * (128 + 2) * 4
