@@ -696,12 +696,14 @@ struct CoopLayout {
   }
 };
 
-// Loop-invariant addressing of the cooperative copy.
+// Loop-invariant addressing of the cooperative copy.  Strides are in bytes
+// and fit 32 bits (the host checks), so a page's address is one 32x32->64
+// multiply-add on the scalar unit.
 struct CoopAddr {
   const uint8_t* kc;      // codes of head h0 (block/page strides below)
   const uint8_t* vc;
   const uint8_t* sp;      // this wave's scale array, head h0
-  int64_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
+  uint32_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
   uint32_t lk, lv, ls;    // lane byte offsets in HBM
   bool s_arr_on;          // this wave copies a scale array (wave-uniform)
   bool s_on;              // this lane copies a scale chunk
@@ -732,37 +734,51 @@ __device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, cons
                : "memory", "m0");
 }
 
-// Issue the copies of the 32-token tile at `tb` into `buf` (this wave's part).
-// Page numbers come through the scalar cache (s_load), so looking one up
-// never waits on the vector-memory counter that tracks the copies in flight.
-template <int D, int NG>
-__device__ __forceinline__ void coop_issue(const CoopAddr& C, int wave, int tb, int t_end,
-                                           uint8_t* buf) {
-  using L = CoopLayout<D, NG>;
+// Pages and in-page offsets of the two 16-token halves of the tile at `tb`,
+// read through the scalar cache (s_load): a lookup never waits on the
+// vector-memory counter that tracks the copies in flight.  A second half
+// wholly past the end re-reads the first half's page (its tokens are masked).
+struct TilePages {
+  uint32_t page[2];
+  uint32_t off[2];
+};
+
+__device__ __forceinline__ TilePages tile_pages(const CoopAddr& C, int tb, int t_end) {
   const bt_scalar_t bt = (bt_scalar_t)(C.bt);
-  int64_t page[2], off[2];
+  TilePages p;
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    // a second half wholly past the end re-reads the first half's page (masked)
     const int pb = (x == 0 || tb + 16 < t_end) ? tb + 16 * x : tb;
-    page[x] = bt[pb >> C.bs_shift];
-    off[x] = pb & ((1 << C.bs_shift) - 1);
+    p.page[x] = static_cast<uint32_t>(bt[pb >> C.bs_shift]);
+    p.off[x] = static_cast<uint32_t>(pb & ((1 << C.bs_shift) - 1));
   }
+  return p;
+}
+
+// Issue this wave's copies of the tile whose pages are P into `buf`.
+template <int D, int NG>
+__device__ __forceinline__ void coop_issue(const CoopAddr& C, int wave, const TilePages& P,
+                                           uint8_t* buf) {
+  using L = CoopLayout<D, NG>;
 #pragma unroll
   for (int j = 0; j < L::NJ; ++j) {
     const int q = wave + 8 * j;                  // 1-KB copy index within the tile
     const int arr = q / (2 * L::CPS);            // 0 = K, 1 = V
     const int x = (q / L::CPS) & 1;
     const int part = q % L::CPS;
-    const uint8_t* base = arr == 0 ? C.kc + (page[x] * C.kc_b + off[x] * C.kc_p)
-                                   : C.vc + (page[x] * C.vc_b + off[x] * C.vc_p);
+    // selects, not indexing: x is only known to be 0 or 1 at run time
+    const uint32_t pg = __builtin_amdgcn_readfirstlane(x ? P.page[1] : P.page[0]);
+    const uint32_t of = __builtin_amdgcn_readfirstlane(x ? P.off[1] : P.off[0]);
+    const uint64_t o = static_cast<uint64_t>(pg) * (arr == 0 ? C.kc_b : C.vc_b) +
+                       of * (arr == 0 ? C.kc_p : C.vc_p);
     uint8_t* dst = buf + (arr == 0 ? L::K_OFF : L::V_OFF) + x * 16 * L::CROW + part * 1024;
-    lds_copy16(base, arr == 0 ? C.lk : C.lv, dst);
+    lds_copy16((arr == 0 ? C.kc : C.vc) + o, arr == 0 ? C.lk : C.lv, dst);
   }
   if (C.s_arr_on) {
-    const int64_t pg = C.s_x ? page[1] : page[0];
-    const int64_t of = C.s_x ? off[1] : off[0];
-    if (C.s_on) lds_copy16(C.sp + (pg * C.sp_b + of * C.sp_p), C.ls, buf + C.s_lds);
+    const uint32_t pg = __builtin_amdgcn_readfirstlane(C.s_x ? P.page[1] : P.page[0]);
+    const uint32_t of = __builtin_amdgcn_readfirstlane(C.s_x ? P.off[1] : P.off[0]);
+    const uint64_t o = static_cast<uint64_t>(pg) * C.sp_b + of * C.sp_p;
+    if (C.s_on) lds_copy16(C.sp + o, C.ls, buf + C.s_lds);
   }
 }
 
@@ -840,9 +856,10 @@ __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int co
     }
 }
 
-// One tile, software-pipelined with the previous one: read this wave's slice
-// of tile i from `cur`, start the copy of tile i + NBUF - 1 into `nxt` (the
-// buffer tile i - 1 used), then QK and scores of tile i next to PV of tile
+// One tile, software-pipelined with the previous one: start the copy of tile
+// i + NBUF - 1 into `nxt` (the buffer tile i - 1 used; its pages were looked
+// up during the previous tile), look up the pages of tile i + NBUF, read this
+// wave's slice of tile i from `cur`, then QK and scores of tile i next to PV of tile
 // i - 1 (independent work for the matrix cores while the VALU converts and
 // scales), the running-max update, and P' of tile i, which PV consumes in
 // the next call.  Ends with a wait for this wave's copies of tile i + 1 and
@@ -852,14 +869,16 @@ __device__ __forceinline__ void coop_tile(WaveState<D / 32, NG, KASYM, VASYM>& W
                                           const CoopAddr& C, int i, int ntiles, int t_begin,
                                           int t_end, int wave, int col, int blk,
                                           const uint8_t* cur, uint8_t* nxt, uint32_t (&vw)[2][4],
-                                          h8& ahi, h8& alo) {
+                                          h8& ahi, h8& alo, TilePages& pages) {
   constexpr int NCH = D / 32;
   const int tb = t_begin + 32 * i;
+  // `nxt` was last read by tile i - 1, before the previous barrier
+  if (i + NBUF - 1 < ntiles) coop_issue<D, NG>(C, wave, pages, nxt);
+  if (i + NBUF < ntiles) pages = tile_pages(C, tb + 32 * NBUF, t_end);
   SubTile<NCH, NG> st[2];
   uint32_t vn[2][4];
   coop_read<D, NG, KASYM, VASYM>(cur, wave, col, blk, st);
   coop_read_v<D, NG>(cur, wave, col, blk, vn);
-  if (i + NBUF - 1 < ntiles) coop_issue<D, NG>(C, wave, tb + 32 * (NBUF - 1), t_end, nxt);
   bool valid[2] = {true, true};
   if constexpr (MASK) {
     valid[0] = tb + col < t_end;
@@ -912,8 +931,10 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     const knlp_kv_plane& V = a.vp;
     C.kc = static_cast<const uint8_t*>(K.data) + h0 * K.stride_head;
     C.vc = static_cast<const uint8_t*>(V.data) + h0 * V.stride_head;
-    C.kc_b = K.stride_block; C.kc_p = K.stride_page;
-    C.vc_b = V.stride_block; C.vc_p = V.stride_page;
+    C.kc_b = static_cast<uint32_t>(K.stride_block);
+    C.kc_p = static_cast<uint32_t>(K.stride_page);
+    C.vc_b = static_cast<uint32_t>(V.stride_block);
+    C.vc_p = static_cast<uint32_t>(V.stride_page);
     // code copy: lane -> LDS byte part*1024 + 16*lane of a sub-tile, which
     // holds logical chunk (physical chunk) ^ row of that row
     {
@@ -940,8 +961,8 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     C.s_arr_on = arr_on;
     C.s_on = arr_on && 16 * lane < 16 * L::SROW;
     C.sp = arr_on ? reinterpret_cast<const uint8_t*>(base + h0 * sh) : nullptr;
-    C.sp_b = 2 * sbk;
-    C.sp_p = 2 * spg;
+    C.sp_b = static_cast<uint32_t>(2 * sbk);
+    C.sp_p = static_cast<uint32_t>(2 * spg);
     {
       const int byte = 16 * lane;
       const int r = byte / L::SROW;
@@ -956,7 +977,9 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   const int ntiles = (t_end - t_begin + 31) / 32;
 #pragma unroll
   for (int t = 0; t < NBUF - 1; ++t)
-    if (t < ntiles) coop_issue<D, NG>(C, wave, t_begin + 32 * t, t_end, lds[t]);
+    if (t < ntiles) coop_issue<D, NG>(C, wave, tile_pages(C, t_begin + 32 * t, t_end), lds[t]);
+  TilePages pages{};
+  if (NBUF - 1 < ntiles) pages = tile_pages(C, t_begin + 32 * (NBUF - 1), t_end);
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
@@ -967,7 +990,7 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
 #define KNLP_COOP_TILE(MASK, PV_PREV)                                                     \
   coop_tile<D, NG, KASYM, VASYM, NBUF, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, \
                                                       col, blk, lds[i % NBUF],            \
-                                                      lds[(i + NBUF - 1) % NBUF], vw, ahi, alo)
+                                                      lds[(i + NBUF - 1) % NBUF], vw, ahi, alo, pages)
   int i = 0;
   if (nfull > 0) {
     KNLP_COOP_TILE(false, false);
@@ -1007,10 +1030,11 @@ static bool coop_layout_ok(const knlp_kv_plane& P, int head_size, int num_kv_hea
   const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   if (num_kv_heads % 8 != 0) return false;
   if (!a16(P.data) || P.stride_head != head_size / 2 || P.stride_block % 16 != 0 ||
-      P.stride_page % 16 != 0)
+      P.stride_page % 16 != 0 || P.stride_block >= (1LL << 31) || P.stride_page >= (1LL << 31))
     return false;
   const auto scales_ok = [&](const void* p, int64_t sb, int64_t sp, int64_t sh) {
-    return a16(p) && sh == ng && (2 * sb) % 16 == 0 && (2 * sp) % 16 == 0;
+    return a16(p) && sh == ng && (2 * sb) % 16 == 0 && (2 * sp) % 16 == 0 &&
+           2 * sb < (1LL << 31) && 2 * sp < (1LL << 31);
   };
   if (!scales_ok(P.scales, P.s_stride_block, P.s_stride_page, P.s_stride_head)) return false;
   if (P.format == KNLP_KV_INT4_ASYM &&
