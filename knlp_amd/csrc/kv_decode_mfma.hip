@@ -195,6 +195,10 @@ struct PageWindow {
     first = first_idx;
     const int idx = first_idx + lane;
     win = idx <= last ? bt[idx] : 0;
+    // wait here, inside the (rare) refill, so that the compiler does not put
+    // a vector-memory wait in front of every lookup; in the cooperative
+    // kernel such a wait would also drain the tile copies in flight
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
   }
   __device__ __forceinline__ int64_t page(const int32_t* bt, int lane, int idx) {
     if (idx - first >= kWave) fill(bt, lane, idx);      // uniform branch
@@ -715,7 +719,6 @@ struct CoopAddr {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-typedef const __attribute__((address_space(4))) int32_t* bt_scalar_t;
 
 // 16 bytes per lane from a raw buffer straight into LDS at m0 + 16 * lane.
 // Written as inline asm so that the compiler does not track these copies:
@@ -734,22 +737,23 @@ __device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, cons
                : "memory", "m0");
 }
 
-// Pages and in-page offsets of the two 16-token halves of the tile at `tb`,
-// read through the scalar cache (s_load): a lookup never waits on the
-// vector-memory counter that tracks the copies in flight.  A second half
+// Pages and in-page offsets of the two 16-token halves of the tile at `tb`.
+// Page numbers come from the lane-held block-table window by v_readlane: no
+// memory wait at all, except when the window moves on (every 64 pages),
+// whose refill waits for its own load inside the refill.  A second half
 // wholly past the end re-reads the first half's page (its tokens are masked).
 struct TilePages {
   uint32_t page[2];
   uint32_t off[2];
 };
 
-__device__ __forceinline__ TilePages tile_pages(const CoopAddr& C, int tb, int t_end) {
-  const bt_scalar_t bt = (bt_scalar_t)(C.bt);
+__device__ __forceinline__ TilePages tile_pages(const CoopAddr& C, PageWindow& PW, int lane,
+                                                int tb, int t_end) {
   TilePages p;
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     const int pb = (x == 0 || tb + 16 < t_end) ? tb + 16 * x : tb;
-    p.page[x] = static_cast<uint32_t>(bt[pb >> C.bs_shift]);
+    p.page[x] = static_cast<uint32_t>(PW.page(C.bt, lane, pb >> C.bs_shift));
     p.off[x] = static_cast<uint32_t>(pb & ((1 << C.bs_shift) - 1));
   }
   return p;
@@ -857,9 +861,8 @@ __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int co
 }
 
 // One tile, software-pipelined with the previous one: start the copy of tile
-// i + NBUF - 1 into `nxt` (the buffer tile i - 1 used; its pages were looked
-// up during the previous tile), look up the pages of tile i + NBUF, read this
-// wave's slice of tile i from `cur`, then QK and scores of tile i next to PV of tile
+// i + NBUF - 1 into `nxt` (the buffer tile i - 1 used), read this wave's
+// slice of tile i from `cur`, then QK and scores of tile i next to PV of tile
 // i - 1 (independent work for the matrix cores while the VALU converts and
 // scales), the running-max update, and P' of tile i, which PV consumes in
 // the next call.  Ends with a wait for this wave's copies of tile i + 1 and
@@ -869,12 +872,12 @@ __device__ __forceinline__ void coop_tile(WaveState<D / 32, NG, KASYM, VASYM>& W
                                           const CoopAddr& C, int i, int ntiles, int t_begin,
                                           int t_end, int wave, int col, int blk,
                                           const uint8_t* cur, uint8_t* nxt, uint32_t (&vw)[2][4],
-                                          h8& ahi, h8& alo, TilePages& pages) {
+                                          h8& ahi, h8& alo, PageWindow& PW, int lane) {
   constexpr int NCH = D / 32;
   const int tb = t_begin + 32 * i;
   // `nxt` was last read by tile i - 1, before the previous barrier
-  if (i + NBUF - 1 < ntiles) coop_issue<D, NG>(C, wave, pages, nxt);
-  if (i + NBUF < ntiles) pages = tile_pages(C, tb + 32 * NBUF, t_end);
+  if (i + NBUF - 1 < ntiles)
+    coop_issue<D, NG>(C, wave, tile_pages(C, PW, lane, tb + 32 * (NBUF - 1), t_end), nxt);
   SubTile<NCH, NG> st[2];
   uint32_t vn[2][4];
   coop_read<D, NG, KASYM, VASYM>(cur, wave, col, blk, st);
@@ -975,11 +978,13 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   }
 
   const int ntiles = (t_end - t_begin + 31) / 32;
+  PageWindow PW;
+  PW.last = (t_end - 1) >> C.bs_shift;
+  PW.fill(C.bt, lane, t_begin >> C.bs_shift);
 #pragma unroll
   for (int t = 0; t < NBUF - 1; ++t)
-    if (t < ntiles) coop_issue<D, NG>(C, wave, tile_pages(C, t_begin + 32 * t, t_end), lds[t]);
-  TilePages pages{};
-  if (NBUF - 1 < ntiles) pages = tile_pages(C, t_begin + 32 * (NBUF - 1), t_end);
+    if (t < ntiles)
+      coop_issue<D, NG>(C, wave, tile_pages(C, PW, lane, t_begin + 32 * t, t_end), lds[t]);
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
@@ -990,7 +995,7 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
 #define KNLP_COOP_TILE(MASK, PV_PREV)                                                     \
   coop_tile<D, NG, KASYM, VASYM, NBUF, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, \
                                                       col, blk, lds[i % NBUF],            \
-                                                      lds[(i + NBUF - 1) % NBUF], vw, ahi, alo, pages)
+                                                      lds[(i + NBUF - 1) % NBUF], vw, ahi, alo, PW, lane)
   int i = 0;
   if (nfull > 0) {
     KNLP_COOP_TILE(false, false);

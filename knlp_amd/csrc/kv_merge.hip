@@ -34,21 +34,41 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
   const int ns = min(num_splits, (n_len + split_tokens - 1) / split_tokens);
   const int64_t row0 = (static_cast<int64_t>(seq) * hq + h) * num_splits;
 
+  // Splits are taken U at a time per wave with every load of the group issued
+  // before any use, so a wave waits for about one memory round trip per
+  // group instead of one per split (ns <= 32 at the benchmark shapes: one
+  // group).
+  constexpr int U = 8;
   float M = -INFINITY, L = 0.0f, o[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) o[e] = 0.0f;
   const bool active = lane * E < D;
-  for (int i = w; i < ns; i += NW) {
-    const float mi = part_ml[2 * (row0 + i)];
-    const float li = part_ml[2 * (row0 + i) + 1];
-    const float mn = fmaxf(M, mi);
-    const float a_old = exp2f(M - mn);
-    const float a_new = exp2f(mi - mn);
-    L = L * a_old + li * a_new;
+  for (int base = w; base < ns; base += NW * U) {
+    float mi[U], li[U], oi[U][E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float oi = active ? part_o[(row0 + i) * D + lane * E + e] : 0.0f;
-      o[e] = o[e] * a_old + oi * a_new;
+    for (int u = 0; u < U; ++u) {
+      const int i = base + NW * u;
+      const bool ok = i < ns;
+      mi[u] = ok ? part_ml[2 * (row0 + i)] : -INFINITY;
+      li[u] = ok ? part_ml[2 * (row0 + i) + 1] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        oi[u][e] = ok && active ? part_o[(row0 + i) * D + lane * E + e] : 0.0f;
+    }
+    float mn = M;
+#pragma unroll
+    for (int u = 0; u < U; ++u) mn = fmaxf(mn, mi[u]);
+    if (mn == -INFINITY) continue;       // nothing in this group (or all empty)
+    const float a_old = exp2f(M - mn);   // 0 when M = -inf
+    L *= a_old;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] *= a_old;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float a = exp2f(mi[u] - mn);  // 0 for the padding entries
+      L = fmaf(li[u], a, L);
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = fmaf(oi[u][e], a, o[e]);
     }
     M = mn;
   }
