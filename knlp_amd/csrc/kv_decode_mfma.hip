@@ -1,39 +1,48 @@
 // Stage 2 (matrix-core path): split-K decode attention over packed INT4 K/V
 // for gfx950, used for the GQA shapes of the benchmark configurations.
 //
-// Same contract as decode_valu_kernel (kv_decode_valu.hip): one wave per
-// (sequence, kv head, split), unnormalised partials (acc, max, sum) in the
-// workspace, softmax in base 2.  Replaces the reference's
-// _fused_int4_decode_kernel (F:656-894) for these shapes.
+// Same contract as decode_valu_kernel (kv_decode_valu.hip): unnormalised
+// partials (acc, max, sum) per (sequence, q head, split) in the workspace,
+// softmax in base 2.  Replaces the reference's _fused_int4_decode_kernel
+// (F:656-894) for these shapes.  Two kernels share the per-wave arithmetic:
+// decode_mfma_kernel (one wave per (sequence, kv head, split), loads straight
+// into VGPRs) and decode_mfma_coop_kernel (8 waves stage whole pages of 8 kv
+// heads through LDS; described further down).
 //
 // Work per wave and 32-token tile (two 16-token sub-tiles); lane l has
 // col = l % 16, blk = l / 16.  "Slot (blk, e)" is element e of lane block blk
 // of an MFMA A/B operand: the contraction index k of that element.  Slots are
 // assigned freely, as long as A and B agree.
 //
+// Code encoding: a nibble n enters the matrix cores as the fp16 whose bit
+// pattern is n, the exact subnormal n * 2^-24, so a dword of 8 nibbles
+// becomes 8 fp16 operands with one shift and one mask per pair.  The
+// matrix cores keep fp16 subnormal inputs, and a product with an fp16 q or P'
+// lands far above the fp32 subnormal range, so nothing is lost; the factor
+// 2^24 is folded into the softmax scale and the final accumulator.
+//
 // QK  v_mfma_f32_16x16x32_f16.  Rows r = g*NG + kg are (q head g, K scale
 //     group kg) pairs, where NG = D / group_size.  Columns are the 16 tokens.
-//     A = q masked to group kg (built once per wave).  B = the K nibbles of
-//     the token, as exact fp16 16 + n.  The lane's 16-byte load (D = 128)
-//     holds 32 nibbles; dword c goes to chunk c.  The accumulator starts at
-//     -16 * sum(q over the group), which cancels the bias.  The output lane
-//     (token col, rows 4blk..4blk+3) then holds sum(q.n) per group, and the
-//     score is  sum_kg s[t,kg] * S + z[t,kg] * sum(q)  in fp32.  This is the
+//     A = q masked to group kg (built once per wave), B = the token's K codes.
+//     Symmetric K starts the accumulator at -8 * 2^-24 * sum(q over the
+//     group).  The output lane (token col, rows 4blk..4blk+3) then holds
+//     2^-24 * sum(q.n) per group, and the score is
+//     sum_kg s[t,kg] * S + z[t,kg] * 2^-24 * sum(q)  in fp32.  This is the
 //     scale placement of docs/fused-quant/fp8-attention-hardware-notes.md:108-113.
 // PV  The V scale depends on the token, which is the contraction index, so
 //     it goes into the probabilities: P'[(g,vg), t] = p[g,t] * s_v[t,vg], split
-//     into fp16 hi + lo (about 22 significant bits).  B = V nibbles as 16 + n;
-//     the bias and the zero-point fold into a per-row term
-//     sum_t p * (z - 16 s), accumulated in fp32.  Output rows are (g, vg)
-//     pairs and columns are head_dim elements; a column's value is kept only
-//     in the row whose vg is the column's group.
+//     into fp16 hi + lo (about 22 significant bits).  B = the V codes; the
+//     zero-point (asymmetric) or -8 s (symmetric) folds into a per-row term
+//     sum_t p * z, accumulated in fp32.  Output rows are (g, vg) pairs and
+//     columns are head_dim elements; a column's value is kept only in the row
+//     whose vg is the column's group.
 // Both operands of PV need "lane = row/column, registers = tokens", but
-// they arrive as "lane = token".  The transposes run on the matrix cores
-// instead of through LDS:
-//   * V: v_mfma_i32_16x16x32_i8 with A = the nibbles as bytes, B = 64 * a
-//     selection matrix, C = 0x4C00.  Each int32 output is then the fp16 bit
-//     pattern of 16 + n for one (token, column).
-//   * P': v_mfma_f32_16x16x16_f16 against the identity.
+// they arrive as "lane = token".  P' is transposed on the matrix cores
+// (v_mfma_f32_16x16x16_f16 against the identity).  V is transposed either
+// on the matrix cores (per-head kernel: v_mfma_i32_16x16x32_i8 with A = the
+// nibbles as bytes and B = a selection matrix, each int32 output then being
+// the code of one (token, column)), or for free by reading the staged tile
+// from LDS in column order (cooperative kernel, pv_columns).
 // Output layout assumed for 16x16 MFMAs (all shapes used here): lane l holds
 // D[4*(l/16) + i][l % 16] in register i.
 //
@@ -90,16 +99,23 @@ __device__ __forceinline__ float row_sum16(float x) {
   return x;
 }
 
+// Masks that pick one nibble per fp16 half of a dword: at bits 0-3 (value n)
+// or at bits 4-7 (value 16 n); both stay inside the fp16 mantissa, so the
+// half is the exact subnormal n * 2^-24 or 16 n * 2^-24.
+constexpr uint32_t kNib1 = 0x000F000Fu;
+constexpr uint32_t kNib16 = 0x00F000F0u;
+
 // 8 nibbles (one dword, element 2i in the low nibble of byte i) -> 8 fp16
-// values in slot order kNibK whose bit patterns are the nibbles themselves:
-// the exact subnormals n * 2^-24.  Seven VALU ops per dword.
+// values in slot order kNibK: even nibbles as n * 2^-24, odd nibbles as
+// 16 n * 2^-24 (slots e with e & 2).  Five VALU ops per dword; the q slots
+// that meet the odd nibbles hold q / 16.
 __device__ __forceinline__ h8 nibbles_to_h8_sub(uint32_t w) {
-  constexpr uint32_t m = 0x000F000Fu;
+  const uint32_t t = w >> 8;
   u4 o;
-  o[0] = w & m;           // n0, n4
-  o[1] = (w >> 4) & m;    // n1, n5
-  o[2] = (w >> 8) & m;    // n2, n6
-  o[3] = (w >> 12) & m;   // n3, n7
+  o[0] = w & kNib1;     // n0, n4
+  o[1] = w & kNib16;    // 16 n1, 16 n5
+  o[2] = t & kNib1;     // n2, n6
+  o[3] = t & kNib16;    // 16 n3, 16 n7
   return __builtin_bit_cast(h8, o);
 }
 
@@ -382,8 +398,10 @@ struct WaveState {
   // of columns (D/16)*col .. (D/16)*col + D/16 - 1 of token 16x + 4blk + i,
   // the tokens of this lane's A slots 4x + i.  Accumulator j = 2c + h holds
   // column d = (D/16) * col + j.  Token pairs are interleaved by halves with
-  // v_perm, then each column's nibble pair is one shift and one mask: the
-  // fp16 subnormal bit patterns of slots (2q, 2q + 1).
+  // v_perm, then each column's nibble pair is one mask (after one shift per
+  // pair of columns): the fp16 subnormal bit patterns of slots (2q, 2q + 1),
+  // n * 2^-24 for even j and 16 n * 2^-24 for odd j (h == 1), so the
+  // accumulators acc[c][1] carry an extra factor 16.
   __device__ __forceinline__ void pv_columns(const uint32_t (&vw)[2][4], const h8& ahi,
                                              const h8& alo) {
     uint32_t u0[4], u1[4];
@@ -401,7 +419,10 @@ struct WaveState {
         const int j = 2 * c + h;
         u4 bw;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bw[q] = ((j < 4 ? u0[q] : u1[q]) >> (4 * (j % 4))) & 0x000F000Fu;
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t u = j < 4 ? u0[q] : u1[q];
+          bw[q] = ((j % 4) < 2 ? u : u >> 8) & (j % 2 ? kNib16 : kNib1);
+        }
         const h8 bv = __builtin_bit_cast(h8, bw);
         acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
         acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
@@ -492,7 +513,10 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const _Float16 v = on ? __builtin_bit_cast(_Float16, qv[8 * c + kNibK[e]]) : _Float16(0);
-        W.aq[c][e] = v;
+        // odd nibbles arrive as 16 n: their q slot holds q / 16 (exact
+        // unless |q| < 2^-10, where the fp16 subnormal keeps an absolute
+        // error below 2^-25)
+        W.aq[c][e] = (e & 2) ? v * static_cast<_Float16>(0.0625f) : v;
         qpart += static_cast<float>(v);
       }
     }
@@ -550,7 +574,8 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
         const int g = r / NG;
         if (g < G && d / gs == r % NG) {
           const int64_t row = (row0 + g) * a.num_splits + split;
-          a.part_o[row * D + d] = fmaf(W.acc[c][h][i], 0x1p24f, W.zacc[i]);
+          // pv_columns' odd columns carry a factor 16
+          a.part_o[row * D + d] = fmaf(W.acc[c][h][i], COLS && h ? 0x1p20f : 0x1p24f, W.zacc[i]);
         }
       }
     }
@@ -677,11 +702,13 @@ struct CoopLayout {
   static constexpr int SROW = kHeads * SB;        // LDS row of one scale array
   static constexpr int CPS = 16 * CROW / 1024;    // 1-KB wave copies per code sub-tile
   static constexpr int NJ = 2 * 2 * CPS / 8;      // code copies per wave and tile
+  static constexpr int NPW = NJ / 2;              // code parts per wave, array and tile
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = 2 * 16 * CROW;
   static constexpr int S_OFF = 4 * 16 * CROW;     // 4 arrays (ks, vs, kz, vz) x 2 sub-tiles
   static constexpr int BYTES = S_OFF + 8 * 16 * SROW;
-  static_assert(8 % CPS == 0 && NJ >= 1, "code sub-tiles split evenly over the 8 waves");
+  static_assert(CPS % 4 == 0 && NPW >= 1 && NPW <= 2,
+                "each sub-tile's code parts split evenly over its 4 waves");
   static_assert(16 * SROW <= 1024, "one wave copy per scale sub-tile");
   // Rows are not padded; bank conflicts are avoided by XOR swizzles, so two
   // blocks' double buffers fit one CU's LDS.  The 16-byte chunk c of code
@@ -702,16 +729,19 @@ struct CoopLayout {
 
 // Loop-invariant addressing of the cooperative copy.  Strides are in bytes
 // and fit 32 bits (the host checks), so a page's address is one 32x32->64
-// multiply-add on the scalar unit.
+// multiply-add on the scalar unit.  Wave w copies sub-tile x = w % 2 only:
+// code parts w / 2 (+ 4) of K and V and the scale chunk of array w / 2, so
+// each wave looks up one page per tile.
 struct CoopAddr {
   const uint8_t* kc;      // codes of head h0 (block/page strides below)
   const uint8_t* vc;
   const uint8_t* sp;      // this wave's scale array, head h0
   uint32_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
-  uint32_t lk, lv, ls;    // lane byte offsets in HBM
+  uint32_t lk[2], lv[2], ls;   // lane byte offsets in HBM (code parts, scale chunk)
+  bool same_kv;           // K and V codes share their strides (one page offset)
   bool s_arr_on;          // this wave copies a scale array (wave-uniform)
   bool s_on;              // this lane copies a scale chunk
-  int s_x;                // sub-tile whose scale chunk this wave copies
+  int x;                  // sub-tile this wave copies
   int s_lds;              // LDS offset of this wave's scale sub-tile
   const int32_t* bt;
   int bs_shift;
@@ -720,69 +750,52 @@ struct CoopAddr {
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 
-// 16 bytes per lane from a raw buffer straight into LDS at m0 + 16 * lane.
+// 16 bytes per lane from global memory (64-bit scalar base + 32-bit lane
+// offset) straight into LDS at m0 + 16 * lane.
 // Written as inline asm so that the compiler does not track these copies:
 // its conservative tracking would put a full vector-memory wait before
 // every LDS read, serialising the copies of later tiles with the compute of
 // this one.  All waits for the copies are explicit (wait_vmcnt) and
 // followed by a block barrier before any wave reads the copied bytes.
 __device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, const void* lds_dst) {
+  // base and m0 are wave-uniform; readfirstlane makes that explicit so that
+  // both are allocated to SGPRs
   const uint64_t b = reinterpret_cast<uint64_t>(base);
-  const i4 rsrc = {static_cast<int>(b), static_cast<int>((b >> 32) & 0xFFFF), -1, 0x00020000};
-  const uint32_t m0 = static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(lds_dst)));
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  // (readfirstlane returns int: convert through uint32_t, never sign-extend)
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(lds_dst))));
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(voff), "s"(rsrc), "s"(m0)
+               : "v"(voff), "s"(sb), "s"(m0)
                : "memory", "m0");
 }
 
-// Pages and in-page offsets of the two 16-token halves of the tile at `tb`.
-// Page numbers come from the lane-held block-table window by v_readlane: no
-// memory wait at all, except when the window moves on (every 64 pages),
-// whose refill waits for its own load inside the refill.  A second half
-// wholly past the end re-reads the first half's page (its tokens are masked).
-struct TilePages {
-  uint32_t page[2];
-  uint32_t off[2];
-};
-
-__device__ __forceinline__ TilePages tile_pages(const CoopAddr& C, PageWindow& PW, int lane,
-                                                int tb, int t_end) {
-  TilePages p;
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    const int pb = (x == 0 || tb + 16 < t_end) ? tb + 16 * x : tb;
-    p.page[x] = static_cast<uint32_t>(PW.page(C.bt, lane, pb >> C.bs_shift));
-    p.off[x] = static_cast<uint32_t>(pb & ((1 << C.bs_shift) - 1));
-  }
-  return p;
-}
-
-// Issue this wave's copies of the tile whose pages are P into `buf`.
+// Issue this wave's copies of the tile at `tb` into `buf`.  The page number
+// comes from the lane-held block-table window by v_readlane: no memory wait
+// at all, except when the window moves on (every 64 pages), whose refill
+// waits for its own load inside the refill.  A second half wholly past the
+// end re-reads the first half's page (its tokens are masked).
 template <int D, int NG>
-__device__ __forceinline__ void coop_issue(const CoopAddr& C, int wave, const TilePages& P,
-                                           uint8_t* buf) {
+__device__ __forceinline__ void coop_issue(const CoopAddr& C, PageWindow& PW, int lane,
+                                           int wave, int tb, int t_end, uint8_t* buf) {
   using L = CoopLayout<D, NG>;
+  const int pb = (C.x == 0 || tb + 16 < t_end) ? tb + 16 * C.x : tb;
+  const uint32_t pg = static_cast<uint32_t>(PW.page(C.bt, lane, pb >> C.bs_shift));
+  const uint32_t of = static_cast<uint32_t>(pb & ((1 << C.bs_shift) - 1));
+  const uint64_t ok = static_cast<uint64_t>(pg) * C.kc_b + of * C.kc_p;
+  const uint64_t ov = C.same_kv ? ok : static_cast<uint64_t>(pg) * C.vc_b + of * C.vc_p;
+  uint8_t* dst = buf + C.x * 16 * L::CROW + (wave >> 1) * 1024;
 #pragma unroll
-  for (int j = 0; j < L::NJ; ++j) {
-    const int q = wave + 8 * j;                  // 1-KB copy index within the tile
-    const int arr = q / (2 * L::CPS);            // 0 = K, 1 = V
-    const int x = (q / L::CPS) & 1;
-    const int part = q % L::CPS;
-    // selects, not indexing: x is only known to be 0 or 1 at run time
-    const uint32_t pg = __builtin_amdgcn_readfirstlane(x ? P.page[1] : P.page[0]);
-    const uint32_t of = __builtin_amdgcn_readfirstlane(x ? P.off[1] : P.off[0]);
-    const uint64_t o = static_cast<uint64_t>(pg) * (arr == 0 ? C.kc_b : C.vc_b) +
-                       of * (arr == 0 ? C.kc_p : C.vc_p);
-    uint8_t* dst = buf + (arr == 0 ? L::K_OFF : L::V_OFF) + x * 16 * L::CROW + part * 1024;
-    lds_copy16((arr == 0 ? C.kc : C.vc) + o, arr == 0 ? C.lk : C.lv, dst);
+  for (int k = 0; k < L::NPW; ++k) {
+    lds_copy16(C.kc + ok, C.lk[k], dst + L::K_OFF + k * 4096);
+    lds_copy16(C.vc + ov, C.lv[k], dst + L::V_OFF + k * 4096);
   }
   if (C.s_arr_on) {
-    const uint32_t pg = __builtin_amdgcn_readfirstlane(C.s_x ? P.page[1] : P.page[0]);
-    const uint32_t of = __builtin_amdgcn_readfirstlane(C.s_x ? P.off[1] : P.off[0]);
-    const uint64_t o = static_cast<uint64_t>(pg) * C.sp_b + of * C.sp_p;
-    if (C.s_on) lds_copy16(C.sp + o, C.ls, buf + C.s_lds);
+    const uint64_t os = static_cast<uint64_t>(pg) * C.sp_b + of * C.sp_p;
+    if (C.s_on) lds_copy16(C.sp + os, C.ls, buf + C.s_lds);
   }
 }
 
@@ -864,8 +877,8 @@ __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int co
 // i + NBUF - 1 into `nxt` (the buffer tile i - 1 used), read this wave's
 // slice of tile i from `cur`, then QK and scores of tile i next to PV of tile
 // i - 1 (independent work for the matrix cores while the VALU converts and
-// scales), the running-max update, and P' of tile i, which PV consumes in
-// the next call.  Ends with a wait for this wave's copies of tile i + 1 and
+// scales), tile i's V into the registers that PV has just consumed, the
+// running-max update, and P' of tile i, which PV consumes in the next call.  Ends with a wait for this wave's copies of tile i + 1 and
 // a block barrier, after which every wave's copies of tile i + 1 have landed.
 template <int D, int NG, bool KASYM, bool VASYM, int NBUF, bool MASK, bool PV_PREV>
 __device__ __forceinline__ void coop_tile(WaveState<D / 32, NG, KASYM, VASYM>& W,
@@ -876,12 +889,9 @@ __device__ __forceinline__ void coop_tile(WaveState<D / 32, NG, KASYM, VASYM>& W
   constexpr int NCH = D / 32;
   const int tb = t_begin + 32 * i;
   // `nxt` was last read by tile i - 1, before the previous barrier
-  if (i + NBUF - 1 < ntiles)
-    coop_issue<D, NG>(C, wave, tile_pages(C, PW, lane, tb + 32 * (NBUF - 1), t_end), nxt);
+  if (i + NBUF - 1 < ntiles) coop_issue<D, NG>(C, PW, lane, wave, tb + 32 * (NBUF - 1), t_end, nxt);
   SubTile<NCH, NG> st[2];
-  uint32_t vn[2][4];
   coop_read<D, NG, KASYM, VASYM>(cur, wave, col, blk, st);
-  coop_read_v<D, NG>(cur, wave, col, blk, vn);
   bool valid[2] = {true, true};
   if constexpr (MASK) {
     valid[0] = tb + col < t_end;
@@ -890,12 +900,10 @@ __device__ __forceinline__ void coop_tile(WaveState<D / 32, NG, KASYM, VASYM>& W
   float score[2][4 / NG];
   W.template scores<MASK>(st, valid, score);
   if constexpr (PV_PREV) W.pv_columns(vw, ahi, alo);
+  // tile i's V replaces tile i - 1's in place once its PV has consumed it
+  coop_read_v<D, NG>(cur, wave, col, blk, vw);
   if (W.max_moves(score)) W.raise_max(score);
   W.template probs<MASK>(st, valid, score, ahi, alo);
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) vw[x][k] = vn[x][k];
   // copies issued after tile i + 1's: tiles i + 2 .. min(i + NBUF - 1, ntiles - 1)
   wait_tile_copies<CoopLayout<D, NG>::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
   __syncthreads();
@@ -938,18 +946,20 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     C.kc_p = static_cast<uint32_t>(K.stride_page);
     C.vc_b = static_cast<uint32_t>(V.stride_block);
     C.vc_p = static_cast<uint32_t>(V.stride_page);
+    C.same_kv = K.stride_block == V.stride_block && K.stride_page == V.stride_page;
     // code copy: lane -> LDS byte part*1024 + 16*lane of a sub-tile, which
     // holds logical chunk (physical chunk) ^ row of that row
-    {
-      const int byte = (wave % L::CPS) * 1024 + 16 * lane;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int byte = ((wave >> 1) + 4 * k) % L::CPS * 1024 + 16 * lane;
       const int r = byte / L::CROW;
       const int c = ((byte % L::CROW) >> 4) ^ r;
-      C.lk = static_cast<uint32_t>(r * K.stride_page + 16 * c);
-      C.lv = static_cast<uint32_t>(r * V.stride_page + 16 * c);
+      C.lk[k] = static_cast<uint32_t>(r * K.stride_page + 16 * c);
+      C.lv[k] = static_cast<uint32_t>(r * V.stride_page + 16 * c);
     }
     // wave w copies scale array w / 2 (ks, vs, kz, vz) of sub-tile w % 2
     const int arr = wave >> 1;
-    C.s_x = wave & 1;
+    C.x = wave & 1;
     const uint16_t* base = arr == 0 ? static_cast<const uint16_t*>(K.scales)
                          : arr == 1 ? static_cast<const uint16_t*>(V.scales)
                          : arr == 2 ? static_cast<const uint16_t*>(K.zeros)
@@ -972,7 +982,7 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
       const int c = ((byte % L::SROW) >> 4) ^ L::scale_swz(r);
       C.ls = static_cast<uint32_t>(r * C.sp_p + 16 * c);
     }
-    C.s_lds = L::S_OFF + (arr * 2 + C.s_x) * 16 * L::SROW;
+    C.s_lds = L::S_OFF + (arr * 2 + C.x) * 16 * L::SROW;
     C.bt = a.block_table + seq * a.bt_stride;
     C.bs_shift = a.block_shift;
   }
@@ -984,7 +994,7 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
 #pragma unroll
   for (int t = 0; t < NBUF - 1; ++t)
     if (t < ntiles)
-      coop_issue<D, NG>(C, wave, tile_pages(C, PW, lane, t_begin + 32 * t, t_end), lds[t]);
+      coop_issue<D, NG>(C, PW, lane, wave, t_begin + 32 * t, t_end, lds[t]);
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
