@@ -247,8 +247,8 @@ def run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, steps, part
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -341,6 +341,8 @@ def main(argv=None):
                      append=append)
     ms_step = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.steps,
                                append=append)
+    run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, max(args.warmup // 4, 1),
+                     partial_only=True)
     ms_partial = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.steps,
                                   partial_only=True)
     print(f"# int4 step {ms_step * 1e3:.1f} us, partial {ms_partial * 1e3:.1f} us",

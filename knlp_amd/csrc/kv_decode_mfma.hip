@@ -49,7 +49,6 @@
 // Online softmax: a row's running max is raised only when a tile's max
 // exceeds it by more than 2 (log2 units).  Then p <= 4 and |P'| <= 4 * s_v,
 // which stays inside fp16 range for any finite fp16 K/V input (s_v < 9400).
-#include <cstdlib>
 
 #include "kv_decode.h"
 
@@ -1065,11 +1064,6 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const bool coop = coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
                     coop_layout_ok(a.vp, head_size, a.num_kv_heads);
   const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
-  static const int nbuf = [] {
-    const char* e = getenv("KNLP_COOP_BUFFERS");
-    const int n = e ? atoi(e) : 4;
-    return n == 2 || n == 3 ? n : 4;
-  }();
   const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
   const dim3 block(kWave * hpb);
 #define KNLP_MFMA_K(KERNEL, D, NG, ...)                                                  \
@@ -1083,12 +1077,8 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
     hipLaunchKernelGGL((KERNEL<D, NG, false, false __VA_ARGS__>), grid, block, 0, stream, a);
 #define KNLP_MFMA(D, NG)                                                                 \
   if (head_size == D && ng == NG) {                                                      \
-    if (coop && nbuf == 4) {                                                             \
+    if (coop) {                                                                          \
       KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG, , 4)                                   \
-    } else if (coop && nbuf == 2) {                                                      \
-      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG, , 2)                                   \
-    } else if (coop) {                                                                   \
-      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG, , 3)                                   \
     } else {                                                                             \
       KNLP_MFMA_K(decode_mfma_kernel, D, NG)                                             \
     }                                                                                    \
