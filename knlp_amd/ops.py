@@ -154,6 +154,25 @@ def reshape_and_cache_v_int8(value, value_cache_int8, v_scales, slot_mapping, *,
     _append(None, value, None, vp, slot_mapping, 0.0, value_cache_int8.shape[1])
 
 
+def reshape_and_cache_fp16(key, value, key_cache, value_cache, slot_mapping) -> None:
+    """Plain fp16 K and V rows into fp16 paged caches at ``slot_mapping``
+    (``slot < 0`` skipped).  Not a function of the reference module: it is
+    the write vLLM's ``reshape_and_cache_flash`` does for the fp16 planes
+    (F:2535-2544), on this library's append kernel.  Either side may be
+    None."""
+    _require_cuda(key, value, key_cache, value_cache, slot_mapping)
+    src = key if key is not None else value
+    if src is None:
+        raise ValueError("reshape_and_cache_fp16 needs key or value")
+    if src.dtype != torch.float16:
+        raise ValueError("reshape_and_cache_fp16 writes fp16 caches from fp16 rows")
+    head_size = src.shape[2]
+    kp = _plane(key_cache, None, None, KV_FP16, head_size) if key is not None else None
+    vp = _plane(value_cache, None, None, KV_FP16, head_size) if value is not None else None
+    block_size = (key_cache if key is not None else value_cache).shape[1]
+    _append(key, value, kp, vp, slot_mapping, 0.0, block_size)
+
+
 def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, num_kv_heads,
             head_size, scale=None, split_tokens=None) -> torch.Tensor:
     _require_cuda(query, block_table, seq_lens)
