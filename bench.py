@@ -5,7 +5,9 @@
 
 * A step is one decode over the whole batch: the split-K partial kernel
   plus the merge kernel.  For config 5 it also includes the quantize-on-append
-  of one new token per sequence.
+  of one new token per sequence, done inside the decode launch
+  (``knlp_kv_append_decode``); the step with the append as separate launches
+  is reported beside it (``append_separate_us_per_step``).
 * Inputs are synthetic and built once, before timing.  Queries and K/V are
   seeded N(0,1) fp16, with 1 % of (kv head, channel) pairs scaled x20 for
   configs 2 and 3.  The caches are filled by this library's append kernel,
@@ -207,9 +209,11 @@ def _cpu_model():
 
 
 def run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, steps, partial_only=False,
-                     append=None):
+                     append=None, fused=None):
     """Launch `steps` decode steps rotating over cache copies; returns the
-    average ms per step measured with events on the current stream."""
+    average ms per step measured with events on the current stream.
+    `append(i)` runs a separate append before each decode; `fused` =
+    (new_k, new_v, slots) appends inside the decode launch instead."""
     import ctypes
     from knlp_amd._lib import lib, check
     from knlp_amd.ops import _stream
@@ -226,7 +230,16 @@ def run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, steps, part
         kp, vp = planes[i % len(planes)]
         if append is not None:
             append(i % len(planes))
-        if partial_only:
+        if fused is not None:
+            nk, nv, sl = fused
+            st = L.knlp_kv_append_decode(
+                q.data_ptr(), 0, q.stride(0), q.stride(1), cfg["B"], cfg["Hq"], cfg["Hkv"],
+                cfg["D"], nk.data_ptr(), nv.data_ptr(), 0, nk.stride(0), nk.stride(1),
+                nv.stride(0), nv.stride(1), sl.data_ptr(), 3, 0.0, ctypes.byref(kp),
+                ctypes.byref(vp), bt_d.data_ptr(), bt_d.stride(0), sl_d.data_ptr(), bs,
+                max_context, scale, split, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), 0,
+                out.stride(0), out.stride(1), stream)
+        elif partial_only:
             st = L.knlp_kv_decode_partial(
                 q.data_ptr(), 0, q.stride(0), q.stride(1), cfg["B"], cfg["Hq"], cfg["Hkv"],
                 cfg["D"], ctypes.byref(kp), ctypes.byref(vp), bt_d.data_ptr(), bt_d.stride(0),
@@ -321,7 +334,7 @@ def main(argv=None):
     ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
     out = torch.empty_like(q)
 
-    append = None
+    append = fused = None
     if cfg["append"]:
         # one new token per sequence per step, written at the next free slot
         new_k = gen_rows(B, Hkv, D, 7000 + c, 0.0, dev)
@@ -336,11 +349,20 @@ def main(argv=None):
             K.reshape_and_cache_v_only_int4(new_v, vcc.data, vcc.scales, app_slots, vcc.zeros,
                                             asymmetric=True, group_size=vcc.gs)
 
+        fused = (new_k, new_v, app_slots)
+
     # ---- INT4 decode: warmup, timed steps, dominant-kernel timing ----------------
+    ms_step_sep = None
+    if fused is not None:
+        # the step with the append as its own launches, for comparison
+        run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.warmup,
+                         append=append)
+        ms_step_sep = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out,
+                                       args.steps, append=append)
     run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.warmup,
-                     append=append)
+                     fused=fused)
     ms_step = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.steps,
-                               append=append)
+                               fused=fused)
     run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, max(args.warmup // 4, 1),
                      partial_only=True)
     ms_partial = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, args.steps,
@@ -434,6 +456,9 @@ def main(argv=None):
                      "avg_launch_us": round(ms_partial * 1e3, 2)},
         "cpu_baseline": cpu,
         "parity_max_abs_vs_oracle": parity,
+        **({"append": "fused into the decode launch (knlp_kv_append_decode)",
+            "append_separate_us_per_step": round(ms_step_sep * 1e3, 2)}
+           if ms_step_sep is not None else {}),
         **res16,
     }
     print(json.dumps(rec))

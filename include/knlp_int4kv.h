@@ -164,6 +164,35 @@ int knlp_kv_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
                    int64_t workspace_bytes, void* out, int32_t out_dtype,
                    int64_t o_stride_seq, int64_t o_stride_head, void* stream);
 
+/*
+ * Fused append + decode for one new token per sequence: quantise the token
+ * being decoded (key / value: [num_seqs, num_kv_heads, head_size] fp16 or
+ * bf16, src_dtype) into the caches at slot_mapping[seq] and run
+ * knlp_kv_decode_partial + knlp_kv_decode_merge, in the same two launches as
+ * knlp_kv_decode.  No counterpart function in the reference: it replaces
+ * the separate reshape_and_cache_* launch (F:418-472, F:603-647,
+ * F:1287-1312, F:1619-1650) that F's backend issues before every decode
+ * (F:2600-2689), the fusion docs/fused-quant/latency.md:41 proposes.
+ * Contract: seq_lens[seq] already counts the new token, and slot_mapping[seq]
+ * is the slot of position seq_lens[seq] - 1 of that sequence (or < 0: no
+ * write); the workgroup whose split holds that position writes the row
+ * before it reads the page, and no other workgroup reads that slot.  The
+ * codes are bit-identical to knlp_kv_append's; key or value may be NULL.
+ */
+int knlp_kv_append_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                          int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t head_size, const void* key,
+                          const void* value, int32_t src_dtype, int64_t key_stride_seq,
+                          int64_t key_stride_head, int64_t value_stride_seq,
+                          int64_t value_stride_head, const void* slot_mapping,
+                          int32_t slot_dtype, float clip_ratio,
+                          const knlp_kv_plane* key_cache, const knlp_kv_plane* value_cache,
+                          const int32_t* block_table, int64_t bt_stride_seq,
+                          const int32_t* seq_lens, int32_t block_size, int32_t max_context,
+                          float softmax_scale, int32_t split_tokens, void* workspace,
+                          int64_t workspace_bytes, void* out, int32_t out_dtype,
+                          int64_t o_stride_seq, int64_t o_stride_head, void* stream);
+
 /* Which decode kernel a shape dispatches to: 1 = MFMA path, 0 = VALU path,
  * negative = unsupported (status).  Lets tests and the bench report it. */
 int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads,

@@ -196,14 +196,19 @@ int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads, int32_
              : 0;
 }
 
-int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
-                           int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
-                           int32_t num_kv_heads, int32_t head_size,
-                           const knlp_kv_plane* key_cache, const knlp_kv_plane* value_cache,
-                           const int32_t* block_table, int64_t bt_stride_seq,
-                           const int32_t* seq_lens, int32_t block_size, int32_t max_context,
-                           float softmax_scale, int32_t split_tokens, void* workspace,
-                           int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Decode partial with an optional fused append of the token being decoded.
+int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                   int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                   int32_t num_kv_heads, int32_t head_size, const knlp_kv_plane* key_cache,
+                   const knlp_kv_plane* value_cache, const int32_t* block_table,
+                   int64_t bt_stride_seq, const int32_t* seq_lens, int32_t block_size,
+                   int32_t max_context, float softmax_scale, int32_t split_tokens,
+                   void* workspace, int64_t workspace_bytes, const AppendArgs* app,
+                   void* stream) {
   if (q_dtype != KNLP_DT_F16 && q_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
   if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
       max_context <= 0 || split_tokens <= 0 || split_tokens % 64)
@@ -250,11 +255,30 @@ int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_
   a.max_context = max_context;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
+  if (app != nullptr) a.app = *app;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (kind == 1 && softmax_scale > 0.0f && mfma_layout_ok(*key_cache, head_size, block_size) &&
       mfma_layout_ok(*value_cache, head_size, block_size))
     return launch_decode_mfma(a, head_size, s);
   return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                           int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_size,
+                           const knlp_kv_plane* key_cache, const knlp_kv_plane* value_cache,
+                           const int32_t* block_table, int64_t bt_stride_seq,
+                           const int32_t* seq_lens, int32_t block_size, int32_t max_context,
+                           float softmax_scale, int32_t split_tokens, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  return decode_partial(query, q_dtype, q_stride_seq, q_stride_head, num_seqs, num_q_heads,
+                        num_kv_heads, head_size, key_cache, value_cache, block_table,
+                        bt_stride_seq, seq_lens, block_size, max_context, softmax_scale,
+                        split_tokens, workspace, workspace_bytes, nullptr, stream);
 }
 
 int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const int32_t* seq_lens,
@@ -294,6 +318,60 @@ int knlp_kv_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
                                   block_table, bt_stride_seq, seq_lens, block_size, max_context,
                                   softmax_scale, split_tokens, workspace, workspace_bytes,
                                   stream);
+  if (st) return st;
+  return knlp_kv_decode_merge(workspace, workspace_bytes, seq_lens, num_seqs, num_q_heads,
+                              head_size, max_context, split_tokens, out, out_dtype, o_stride_seq,
+                              o_stride_head, stream);
+}
+
+int knlp_kv_append_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                          int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t head_size, const void* key,
+                          const void* value, int32_t src_dtype, int64_t key_stride_seq,
+                          int64_t key_stride_head, int64_t value_stride_seq,
+                          int64_t value_stride_head, const void* slot_mapping,
+                          int32_t slot_dtype, float clip_ratio,
+                          const knlp_kv_plane* key_cache, const knlp_kv_plane* value_cache,
+                          const int32_t* block_table, int64_t bt_stride_seq,
+                          const int32_t* seq_lens, int32_t block_size, int32_t max_context,
+                          float softmax_scale, int32_t split_tokens, void* workspace,
+                          int64_t workspace_bytes, void* out, int32_t out_dtype,
+                          int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
+  if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  if (num_seqs > 0 && out == nullptr) return KNLP_ERR_ARG;
+  if (num_seqs == 0) return KNLP_OK;
+  if (src_dtype != KNLP_DT_F16 && src_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  if (slot_dtype != KNLP_DT_I32 && slot_dtype != KNLP_DT_I64) return KNLP_ERR_DTYPE;
+  if (key == nullptr && value == nullptr) return KNLP_ERR_ARG;
+  if (slot_mapping == nullptr) return KNLP_ERR_ARG;
+  if (!(clip_ratio >= 0.0f) || std::isinf(clip_ratio)) return KNLP_ERR_ARG;
+  int st;
+  if (key != nullptr) {
+    if ((st = check_plane(key_cache, head_size, false))) return st;
+    if (key_cache->format == KNLP_KV_FP16 && src_dtype != KNLP_DT_F16) return KNLP_ERR_DTYPE;
+    if (!aligned(key, 4) || key_stride_seq % 2 || key_stride_head % 2) return KNLP_ERR_ALIGN;
+  }
+  if (value != nullptr) {
+    if ((st = check_plane(value_cache, head_size, false))) return st;
+    if (value_cache->format == KNLP_KV_FP16 && src_dtype != KNLP_DT_F16) return KNLP_ERR_DTYPE;
+    if (!aligned(value, 4) || value_stride_seq % 2 || value_stride_head % 2)
+      return KNLP_ERR_ALIGN;
+  }
+  AppendArgs app{};
+  app.key = static_cast<const uint16_t*>(key);
+  app.value = static_cast<const uint16_t*>(value);
+  app.kst = key_stride_seq;
+  app.ksh = key_stride_head;
+  app.vst = value_stride_seq;
+  app.vsh = value_stride_head;
+  app.slots = slot_mapping;
+  app.slots64 = slot_dtype == KNLP_DT_I64;
+  app.src_bf16 = src_dtype == KNLP_DT_BF16;
+  app.clip_ratio = clip_ratio;
+  st = decode_partial(query, q_dtype, q_stride_seq, q_stride_head, num_seqs, num_q_heads,
+                      num_kv_heads, head_size, key_cache, value_cache, block_table,
+                      bt_stride_seq, seq_lens, block_size, max_context, softmax_scale,
+                      split_tokens, workspace, workspace_bytes, &app, stream);
   if (st) return st;
   return knlp_kv_decode_merge(workspace, workspace_bytes, seq_lens, num_seqs, num_q_heads,
                               head_size, max_context, split_tokens, out, out_dtype, o_stride_seq,

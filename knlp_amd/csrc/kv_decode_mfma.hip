@@ -613,6 +613,8 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   const int t_begin = split * a.split_tokens;
   if (t_begin >= seq_len) return;
   const int t_end = min(seq_len, t_begin + a.split_tokens);
+  // the token being decoded, when the caller fused its append into this launch
+  decode_append<D>(a, seq, kvh, split, seq_len, lane);
 
   WaveState<NCH, NG, KASYM, VASYM> W;
   init_wave<D, NG, KASYM, VASYM>(W, a, seq, kvh, col, blk);
@@ -931,6 +933,10 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   const int t_begin = split * a.split_tokens;
   if (t_begin >= seq_len) return;
   const int t_end = min(seq_len, t_begin + a.split_tokens);
+  // the token being decoded, when the caller fused its append into this launch;
+  // the barrier orders every wave's rows before any wave copies the page
+  decode_append<D>(a, seq, kvh, split, seq_len, lane);
+  if (a.app.key != nullptr || a.app.value != nullptr) __syncthreads();
 
   WaveState<NCH, NG, KASYM, VASYM> W;
   init_wave<D, NG, KASYM, VASYM>(W, a, seq, kvh, col, blk);

@@ -93,6 +93,8 @@ __global__ __launch_bounds__(512) void decode_valu_kernel(DecodeArgs a) {
   const int t_begin = split * a.split_tokens;
   if (t_begin >= seq_len) return;                   // split past the end: no partial
   const int t_end = min(seq_len, t_begin + a.split_tokens);
+  // the token being decoded, when the caller fused its append into this launch
+  decode_append<D>(a, seq, kvh, split, seq_len, lane);
   const int tk = lane / TPT;
   const int c = lane % TPT;
   const int G = a.group;

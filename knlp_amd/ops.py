@@ -174,7 +174,7 @@ def reshape_and_cache_fp16(key, value, key_cache, value_cache, slot_mapping) -> 
 
 
 def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, num_kv_heads,
-            head_size, scale=None, split_tokens=None) -> torch.Tensor:
+            head_size, scale=None, split_tokens=None, append=None) -> torch.Tensor:
     _require_cuda(query, block_table, seq_lens)
     if query.dtype not in _SRC_DTYPES:
         raise ValueError(f"query dtype {query.dtype} not supported (fp16 or bf16)")
@@ -205,14 +205,77 @@ def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, 
     if scale is None:
         scale = 1.0 / (head_size ** 0.5)                  # F:924
     dt = _SRC_DTYPES[query.dtype]
-    st = L.knlp_kv_decode(
+    if append is None:
+        st = L.knlp_kv_decode(
+            query.data_ptr(), dt, query.stride(0), query.stride(1), num_seqs, num_heads,
+            num_kv_heads, head_size, ctypes.byref(kp), ctypes.byref(vp),
+            block_table.data_ptr(), block_table.stride(0), seq_lens.data_ptr(), block_size,
+            max_context, float(scale), int(split_tokens), ws.data_ptr(), ws_bytes,
+            out.data_ptr(), dt, out.stride(0), out.stride(1), _stream())
+        check(st, "knlp_kv_decode")
+        return out
+    key, value, slot_mapping, clip_ratio = append
+    src = key if key is not None else value
+    for t in (key, value):
+        if t is not None and (t.dim() != 3 or t.shape[0] < num_seqs or t.stride(2) != 1):
+            raise ValueError("key/value must be [num_seqs, num_kv_heads, head_size], "
+                             "last axis contiguous")
+    slot_mapping = slot_mapping.contiguous()
+    if slot_mapping.numel() < num_seqs:
+        raise ValueError("slot_mapping shorter than num_seqs")
+    st = L.knlp_kv_append_decode(
         query.data_ptr(), dt, query.stride(0), query.stride(1), num_seqs, num_heads,
-        num_kv_heads, head_size, ctypes.byref(kp), ctypes.byref(vp),
-        block_table.data_ptr(), block_table.stride(0), seq_lens.data_ptr(), block_size,
-        max_context, float(scale), int(split_tokens), ws.data_ptr(), ws_bytes,
-        out.data_ptr(), dt, out.stride(0), out.stride(1), _stream())
-    check(st, "knlp_kv_decode")
+        num_kv_heads, head_size,
+        key.data_ptr() if key is not None else None,
+        value.data_ptr() if value is not None else None, _src_dtype(src),
+        key.stride(0) if key is not None else 0, key.stride(1) if key is not None else 0,
+        value.stride(0) if value is not None else 0, value.stride(1) if value is not None else 0,
+        slot_mapping.data_ptr(), _slot_dtype(slot_mapping), float(clip_ratio),
+        ctypes.byref(kp), ctypes.byref(vp), block_table.data_ptr(), block_table.stride(0),
+        seq_lens.data_ptr(), block_size, max_context, float(scale), int(split_tokens),
+        ws.data_ptr(), ws_bytes, out.data_ptr(), dt, out.stride(0), out.stride(1), _stream())
+    check(st, "knlp_kv_append_decode")
     return out
+
+
+_FORMATS = {"int8": KV_INT8_SYM, "fp16": KV_FP16}
+
+
+def _fmt(name: str, asymmetric: bool) -> int:
+    if name == "int4":
+        return KV_INT4_ASYM if asymmetric else KV_INT4_SYM
+    if name not in _FORMATS:
+        raise ValueError(f"unknown cache format {name!r} (int4, int8 or fp16)")
+    return _FORMATS[name]
+
+
+def append_and_decode(query, key, value, slot_mapping, key_cache, value_cache, k_scales,
+                      v_scales, block_table, seq_lens, num_kv_heads, head_size, *,
+                      k_format="int4", v_format="int4", k_zeros=None, v_zeros=None,
+                      asymmetric=False, k_group_size=None, v_group_size=None,
+                      clip_ratio=None, scale=None, split_tokens=None) -> torch.Tensor:
+    """Quantise the token being decoded into the caches and decode, in the
+    launches of one decode (no separate append launch).
+
+    Not a function of the reference module: it fuses the
+    ``reshape_and_cache_*`` call that F's backend makes before every decode
+    (F:2600-2689) into the decode, as docs/fused-quant/latency.md:41
+    proposes.  ``key`` / ``value`` are ``[num_seqs, num_kv_heads, head_size]``
+    rows of the new token (either may be None), ``slot_mapping[s]`` the slot
+    of position ``seq_lens[s] - 1`` (``< 0``: no write).  ``k_format`` /
+    ``v_format`` are "int4" (``asymmetric`` selects zero-points), "int8" or
+    "fp16"; the caches, scales and zeros are the reference's tensors.  The
+    written codes equal those of the separate append; the output equals the
+    decode after it."""
+    _require_cuda(query, key, value, slot_mapping, key_cache, value_cache, k_scales, v_scales)
+    kf, vf = _fmt(k_format, asymmetric), _fmt(v_format, asymmetric)
+    kp = _plane(key_cache, k_scales, k_zeros, kf,
+                head_size if kf == KV_FP16 else (k_group_size or GROUP_SIZE))
+    vp = _plane(value_cache, v_scales, v_zeros, vf,
+                head_size if vf == KV_FP16 else (v_group_size or GROUP_SIZE))
+    clip = OUTLIER_CLIP_RATIO if clip_ratio is None else clip_ratio
+    return _decode(query, kp, vp, key_cache.shape[1], block_table, seq_lens, num_kv_heads,
+                   head_size, scale, split_tokens, append=(key, value, slot_mapping, clip))
 
 
 def fused_int4_decode(query, key_cache, value_cache, k_scales, v_scales, block_table, seq_lens,

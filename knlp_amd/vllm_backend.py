@@ -18,6 +18,10 @@ Same class names, registry name ("FUSED_INT4"), cache-dtype string
 
 What differs, by design for MI355X:
   * the fused decode is this library's split-K HIP decode (knlp_amd.ops);
+  * a pure decode step on the fused path quantises its new token inside the
+    decode launch (ops.append_and_decode), so the separate append launch the
+    reference issues before every decode disappears
+    (docs/fused-quant/latency.md:41); other steps write first, as F does;
   * the fp16 paged short-sequence decode is the same HIP kernel on fp16
     planes (the reference uses FlashAttention-3, absent on ROCm); a bf16
     model's paged cache goes through the reference's own non-FA path,
@@ -271,10 +275,17 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
                                 kv_cache.device)
 
         n_tok = attn_metadata.num_actual_tokens
+        key_3d = value_3d = None
         if not config.REPLACE_CACHE and n_tok > 0 and value.numel() > 0:
             key_3d = key.view(-1, self.num_kv_heads, self.head_size) if key.dim() == 2 else key
             value_3d = value.view(-1, self.num_kv_heads, self.head_size) \
                 if value.dim() == 2 else value
+        # A pure decode step on the fused path quantises its one new token per
+        # sequence inside the decode launch (no separate append launch); every
+        # other step writes first, as F:2600-2689.
+        fuse_append = (key_3d is not None and attn_metadata.max_query_len == 1 and
+                       attn_metadata.max_seq_len >= config.MIN_FUSED_SEQ_LEN)
+        if key_3d is not None and not fuse_append:
             self._write_quantized(key_3d, value_3d, attn_metadata.slot_mapping)
 
         if not self._logged_init:
@@ -293,7 +304,10 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
         if attn_metadata.max_query_len == 1:
             num_seqs = attn_metadata.seq_lens.shape[0]
             dq = query[:num_seqs]
-            if config.REPLACE_CACHE or attn_metadata.max_seq_len >= config.MIN_FUSED_SEQ_LEN:
+            if fuse_append:
+                dout = self._append_and_decode(dq, key_3d, value_3d, key_cache_fp16,
+                                               attn_metadata)
+            elif config.REPLACE_CACHE or attn_metadata.max_seq_len >= config.MIN_FUSED_SEQ_LEN:
                 dout = self._fused_decode(dq, key_cache_fp16, attn_metadata.block_table,
                                           attn_metadata.seq_lens)
             else:
@@ -354,6 +368,27 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
         return ops.fused_int4_decode(q, c.int4_key, c.int4_value, c.k_scales, c.v_scales,
                                      block_table, seq_lens, k_zeros=c.k_zeros,
                                      v_zeros=c.v_zeros, asymmetric=self._asymmetric, **common)
+
+    def _append_and_decode(self, q, key_3d, value_3d, key_cache_fp16, md) -> torch.Tensor:
+        """The step's quantised append and the fused decode in one decode
+        launch (ops.append_and_decode); the same writes and the same output
+        as _write_quantized followed by _fused_decode."""
+        c, kp, vp, asym = self._caches, self._k_precision, self._v_precision, self._asymmetric
+        n = q.shape[0]
+        if kp == "int4":
+            kcache, ks, kz, key = c.int4_key, c.k_scales, c.k_zeros, key_3d[:n]
+        elif kp == "int8":
+            kcache, ks, kz, key = c.int8_key, c.k_int8_scales, None, key_3d[:n]
+        else:                                  # fp16 K: already in the paged cache
+            kcache, ks, kz, key = key_cache_fp16, None, None, None
+        if vp == "int8":
+            vcache, vs, vz = c.int8_value, c.v_int8_scales, None
+        else:
+            vcache, vs, vz = c.int4_value, c.v_scales, c.v_zeros
+        return ops.append_and_decode(
+            q, key, value_3d[:n], md.slot_mapping[:n], kcache, vcache, ks, vs, md.block_table,
+            md.seq_lens, self.num_kv_heads, self.head_size, k_format=kp, v_format=vp,
+            k_zeros=kz, v_zeros=vz, asymmetric=asym, scale=self.scale)
 
     def _paged_decode(self, q, key_cache, value_cache, block_table, seq_lens) -> torch.Tensor:
         """Short sequences from the fp16 paged cache (F:2930-3048)."""

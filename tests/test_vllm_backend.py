@@ -144,8 +144,10 @@ class Recorder:
 
     def __init__(self, monkeypatch, ops_mod):
         self.calls = []
+        self.kwargs = {}
         for name in ("fused_int4_decode", "kint8_vint4_decode", "kint8_vint8_decode",
-                     "kfp16_vint4_decode", "kfp16_vint8_decode", "fp16_paged_decode"):
+                     "kfp16_vint4_decode", "kfp16_vint8_decode", "fp16_paged_decode",
+                     "append_and_decode"):
             monkeypatch.setattr(ops_mod, name, self._decode(name))
         for name in ("reshape_and_cache_int4", "reshape_and_cache_v_only_int4",
                      "reshape_and_cache_k_int8", "reshape_and_cache_v_int8",
@@ -155,6 +157,7 @@ class Recorder:
     def _decode(self, name):
         def f(q, *a, **k):
             self.calls.append(name)
+            self.kwargs[name] = (a, k)
             # row s of the output is filled with 100 + s so placement is visible
             out = torch.empty_like(q)
             for s in range(q.shape[0]):
@@ -198,6 +201,30 @@ WRITES = {
 
 @pytest.mark.parametrize("k,v", PAIRS)
 def test_decode_dispatch_table(vb, monkeypatch, k, v):
+    """Mixed batch (one decode row, one 2-token prefill): the step's writes,
+    then the decode kernel of the (k, v) pair (F:2701-2707)."""
+    rec = Recorder(monkeypatch, vb.ops)
+    impl = make_impl(vb, monkeypatch, k, v)
+    kv = torch.zeros(kv_layout.kv_cache_shape(NB, BS, HKV, D), dtype=torch.float16)
+    md = vb.FusedInt4AttentionMetadata(
+        num_actual_tokens=3, max_query_len=2,
+        query_start_loc=torch.tensor([0, 1, 3], dtype=torch.int32), max_seq_len=60,
+        seq_lens=torch.tensor([60, 2], dtype=torch.int32),
+        block_table=torch.arange(6, dtype=torch.int32).view(2, 3),
+        slot_mapping=torch.tensor([59, 48, 49]))
+    q = torch.randn(3, H * D).half()
+    kk = torch.randn(3, HKV * D).half()
+    out = impl.forward(None, q, kk, kk, kv, md)
+    assert rec.calls == WRITES[(k, v)] + [vb.DECODE_KERNELS[(k, v)]]
+    assert out.shape == (3, H * D) and float(out[0, 0]) == 100.0
+    assert impl.caches.num_blocks(v) == NB
+
+
+@pytest.mark.parametrize("k,v", PAIRS)
+def test_pure_decode_fuses_the_append(vb, monkeypatch, k, v):
+    """A pure decode step on the fused path makes one call: the new token's
+    quantised append inside the decode (the separate write launch of
+    F:2600-2689 disappears); fp16 K is already in the paged cache."""
     rec = Recorder(monkeypatch, vb.ops)
     impl = make_impl(vb, monkeypatch, k, v)
     kv = torch.zeros(kv_layout.kv_cache_shape(NB, BS, HKV, D), dtype=torch.float16)
@@ -205,9 +232,14 @@ def test_decode_dispatch_table(vb, monkeypatch, k, v):
     q = torch.randn(2, H * D).half()
     kk = torch.randn(2, HKV * D).half()
     out = impl.forward(None, q, kk, kk, kv, md)
-    assert rec.calls == WRITES[(k, v)] + [vb.DECODE_KERNELS[(k, v)]]
+    assert rec.calls == ["append_and_decode"]
+    a, kw = rec.kwargs["append_and_decode"]
+    assert kw["k_format"] == k and kw["v_format"] == v
+    assert (a[0] is None) == (k == "fp16")          # the key rows
+    assert torch.equal(a[2], md.slot_mapping)
+    if k == "fp16":
+        assert a[3] is kv[0] or torch.equal(a[3], kv[0])
     assert out.shape == (2, H * D) and float(out[1, 0]) == 101.0
-    assert impl.caches.num_blocks(v) == NB
 
 
 def test_min_fused_seq_len_gate(vb, monkeypatch):
@@ -218,7 +250,7 @@ def test_min_fused_seq_len_gate(vb, monkeypatch):
     impl.forward(None, q, q[:, :HKV * D], q[:, :HKV * D], kv, decode_md(vb, [47, 10], [0, 1]))
     assert rec.calls[-1] == "fp16_paged_decode"
     impl.forward(None, q, q[:, :HKV * D], q[:, :HKV * D], kv, decode_md(vb, [48, 10], [0, 1]))
-    assert rec.calls[-1] == "fused_int4_decode"
+    assert rec.calls[-1] == "append_and_decode"
 
 
 def test_replace_cache_always_fused(vb, monkeypatch):
