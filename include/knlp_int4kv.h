@@ -194,7 +194,11 @@ int knlp_kv_append_decode(const void* query, int32_t q_dtype, int64_t q_stride_s
                           int64_t o_stride_seq, int64_t o_stride_head, void* stream);
 
 /* Which decode kernel a shape dispatches to: 1 = MFMA path, 0 = VALU path,
- * negative = unsupported (status).  Lets tests and the bench report it. */
+ * negative = unsupported (status).  Lets tests and the bench report it.  The
+ * MFMA path's INT8-K and more-than-16-row shapes need densely packed heads
+ * (stride_head = one head's row) and num_kv_heads % 8 == 0; other layouts of
+ * those shapes run on the VALU kernel, which serves at most 8 query heads per
+ * kv head (more return KNLP_ERR_SHAPE at decode time). */
 int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads,
                                int32_t head_size, int32_t k_format,
                                int32_t k_group_size, int32_t v_format,

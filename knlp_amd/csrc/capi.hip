@@ -188,12 +188,13 @@ int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads, int32_
                                int32_t v_group_size, int32_t q_dtype) {
   if (num_kv_heads <= 0 || num_q_heads % num_kv_heads) return KNLP_ERR_SHAPE;
   const int g = num_q_heads / num_kv_heads;
-  if (g > 8) return KNLP_ERR_SHAPE;
   if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
-  return mfma_supported(g, head_size, k_format, k_group_size, v_format, v_group_size,
-                        q_dtype == KNLP_DT_BF16)
-             ? 1
-             : 0;
+  const bool mfma = mfma_supported(g, head_size, k_format, k_group_size, v_format,
+                                   v_group_size, q_dtype == KNLP_DT_BF16);
+  // the VALU kernel serves up to 8 query heads per kv head; the matrix-core
+  // kernel up to two 16-row head sets (on dense cache layouts)
+  if (g > 8 && !mfma) return KNLP_ERR_SHAPE;
+  return mfma ? 1 : 0;
 }
 
 }  // extern "C"

@@ -118,6 +118,25 @@ __device__ __forceinline__ h8 nibbles_to_h8_sub(uint32_t w) {
   return __builtin_bit_cast(h8, o);
 }
 
+// slot e of a converted INT8 dword pair -> byte index within the pair
+__device__ constexpr int kByteK8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+
+// 8 int8 codes (two dwords, element i in byte i) -> 8 fp16 values in slot
+// order kByteK8 whose bit patterns are the codes biased by 128 (the xor with
+// 0x80 flips the sign bit): the exact subnormals (n + 128) * 2^-24, all below
+// 2^-14.  Four VALU ops per dword; the bias leaves 128 * sum(q) per row, which
+// the accumulator's start value cancels.
+__device__ __forceinline__ h8 bytes_to_h8_sub(uint32_t w0, uint32_t w1) {
+  constexpr uint32_t m = 0x00FF00FFu;
+  const uint32_t a = w0 ^ 0x80808080u, b = w1 ^ 0x80808080u;
+  u4 o;
+  o[0] = a & m;           // bytes 0, 2
+  o[1] = (a >> 8) & m;    // bytes 1, 3
+  o[2] = b & m;           // bytes 4, 6
+  o[3] = (b >> 8) & m;    // bytes 5, 7
+  return __builtin_bit_cast(h8, o);
+}
+
 // nibbles of one dword as 8 int8 slots: [n0 n2 n4 n6 | n1 n3 n5 n7]
 __device__ __forceinline__ long nibbles_to_i8x8(uint32_t w) {
   const uint64_t lo = w & 0x0F0F0F0Fu;
@@ -157,7 +176,20 @@ struct Halves<1> {
 };
 
 template <int NCH>
-struct Codes;    // NCH dwords of packed nibbles (D/8 bytes) per lane and token
+struct Codes;    // NCH dwords of codes per lane and token
+template <>
+struct Codes<8> {
+  uint4 v, w;
+  __device__ uint32_t dw(int c) const {
+    const uint4& u = c < 4 ? v : w;
+    const int i = c & 3;
+    return i == 0 ? u.x : i == 1 ? u.y : i == 2 ? u.z : u.w;
+  }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0));
+  }
+};
 template <>
 struct Codes<4> {
   uint4 v;
@@ -175,10 +207,15 @@ struct Codes<2> {
   }
 };
 
-template <int NCH, int NG>
+// One 16-token sub-tile in the per-lane layout.  K: KCH code dwords and NGK
+// scale halves per row (packed INT4: KCH = NCH, NGK = NG; INT8: KCH = 2 NCH
+// and NGK scale groups, 1 for one scale per row); V: packed INT4.
+template <int NCH, int NG, int KCH = NCH, int NGK = NG>
 struct SubTile {
-  Codes<NCH> k, v;
-  Halves<NG> ks, kz, vs, vz;
+  Codes<KCH> k;
+  Codes<NCH> v;
+  Halves<NGK> ks;
+  Halves<NG> kz, vs, vz;
 };
 
 // Per-wave addressing: uniform bases (this kv head folded in) plus
@@ -242,12 +279,19 @@ __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane,
 // the general path: masked scores, raise_max, masked accumulate.  Both paths
 // do the same arithmetic on rows whose max does not move, so the result does
 // not depend on which path a tile took.
-template <int NCH, int NG, bool KASYM, bool VASYM>
+template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH, int NGK = NG>
 struct WaveState {
   static constexpr int GPL = 4 / NG;
+  // INT8 K codes: two dwords per QK chunk, one scale per NG / NGK row groups
+  static constexpr bool K8 = KCH == 2 * NCH;
+  using ST = SubTile<NCH, NG, KCH, NGK>;
+  static constexpr bool KZ_USED = KASYM;
+  static constexpr bool VZ_USED = VASYM;
+  static_assert(NG % NGK == 0 && (K8 || NGK == NG), "K scale groups nest in the row groups");
   h8 aq[NCH];          // masked q, A operands of QK (row = col)
   float qsum24[4];     // 2^-24 * sum of q over the group of rows 4blk..4blk+3
-  f4 cinit;            // QK accumulator start: 0, or -8 * qsum24 for symmetric K
+  f4 cinit;            // QK accumulator start: 0 for asymmetric INT4 K, else -bias * qsum24
+                       // (bias 8 for symmetric INT4, 128 for the biased INT8 codes)
   h4 eye;              // identity, B operand of the P' transpose
   long vsel[2];        // selection, B operand of the V transpose
   f4 acc[NCH][2];      // PV accumulators (units of 2^-24), rows (g, vg) x columns d
@@ -260,15 +304,18 @@ struct WaveState {
   // Scores of the two sub-tiles in units of 2^-24:
   //   sum_kg s[t,kg] * S[(g,kg),t] + z[t,kg] * qsum24[(g,kg)].
   template <bool MASK>
-  __device__ __forceinline__ void scores(const SubTile<NCH, NG> (&st)[2], const bool (&valid)[2],
+  __device__ __forceinline__ void scores(const ST (&st)[2], const bool (&valid)[2],
                                          float (&score)[2][GPL]) const {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       f4 S = KASYM ? f4{0.f, 0.f, 0.f, 0.f} : cinit;
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[c], nibbles_to_h8_sub(st[x].k.dw(c)), S,
-                                                   0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            aq[c],
+            K8 ? bytes_to_h8_sub(st[x].k.dw(2 * c), st[x].k.dw(2 * c + 1))
+               : nibbles_to_h8_sub(st[x].k.dw(c)),
+            S, 0, 0, 0);
 #pragma unroll
       for (int gi = 0; gi < GPL; ++gi) {
         float sc = 0.0f;
@@ -276,7 +323,7 @@ struct WaveState {
         for (int kg = 0; kg < NG; ++kg) {
           const int i = gi * NG + kg;
           if constexpr (KASYM) sc = fmaf(st[x].kz.get(kg), qsum24[i], sc);
-          sc = fmaf(st[x].ks.get(kg), S[i], sc);
+          sc = fmaf(st[x].ks.get(kg * NGK / NG), S[i], sc);
         }
         score[x][gi] = (MASK && !valid[x]) ? -INFINITY : sc;
       }
@@ -319,7 +366,7 @@ struct WaveState {
   // the PV A operand (lane = row (g, vg), slots = tokens), and the
   // zero-point term, for the two sub-tiles.
   template <bool MASK>
-  __device__ __forceinline__ void probs(const SubTile<NCH, NG> (&st)[2], const bool (&valid)[2],
+  __device__ __forceinline__ void probs(const ST (&st)[2], const bool (&valid)[2],
                                         const float (&score)[2][GPL], h8& ahi, h8& alo) {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
@@ -370,7 +417,7 @@ struct WaveState {
 
   // PV with V transposed on the matrix cores (V arrives as lane = token):
   // accumulator (c, h) holds column d = (D/4)(col/4) + 8c + 2(col%4) + h.
-  __device__ __forceinline__ void pv_transposed(const SubTile<NCH, NG> (&st)[2], const h8& ahi,
+  __device__ __forceinline__ void pv_transposed(const ST (&st)[2], const h8& ahi,
                                                 const h8& alo) {
     const i4 vzero = {0, 0, 0, 0};
 #pragma unroll
@@ -430,7 +477,7 @@ struct WaveState {
   }
 
   template <bool MASK>
-  __device__ __forceinline__ void accumulate(const SubTile<NCH, NG> (&st)[2],
+  __device__ __forceinline__ void accumulate(const ST (&st)[2],
                                              const bool (&valid)[2],
                                              const float (&score)[2][GPL]) {
     h8 ahi, alo;
@@ -439,7 +486,7 @@ struct WaveState {
   }
 
   template <bool MASK>
-  __device__ __forceinline__ void accumulate_cols(const SubTile<NCH, NG> (&st)[2],
+  __device__ __forceinline__ void accumulate_cols(const ST (&st)[2],
                                                   const uint32_t (&vw)[2][4],
                                                   const bool (&valid)[2],
                                                   const float (&score)[2][GPL]) {
@@ -450,7 +497,7 @@ struct WaveState {
 
   // General step: any tile, masked or not, max moving or not.
   template <bool MASK>
-  __device__ __forceinline__ void step(const SubTile<NCH, NG> (&st)[2], int tbase, int t_end,
+  __device__ __forceinline__ void step(const ST (&st)[2], int tbase, int t_end,
                                        int col) {
     bool valid[2] = {true, true};
     if constexpr (MASK) {
@@ -464,7 +511,7 @@ struct WaveState {
   }
 
   template <bool MASK>
-  __device__ __forceinline__ void step_cols(const SubTile<NCH, NG> (&st)[2],
+  __device__ __forceinline__ void step_cols(const ST (&st)[2],
                                             const uint32_t (&vw)[2][4], int tbase, int t_end,
                                             int col) {
     bool valid[2] = {true, true};
@@ -479,23 +526,33 @@ struct WaveState {
   }
 };
 
-// q, constants and accumulators of the wave serving kv head `kvh`.
-template <int D, int NG, bool KASYM, bool VASYM>
-__device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W,
+// Query heads per head set: a set fills the 16 rows of one 16x16 MFMA.
+template <int NG>
+__host__ __device__ constexpr int heads_per_set() { return 16 / NG; }
+
+// q, constants and accumulators of the wave serving kv head `kvh`, for the
+// head set whose first query head (within the kv head's group) is `hs`.
+template <int D, int NG, bool KASYM, bool VASYM, int KCH = D / 32, int NGK = NG>
+__device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK>& W,
                                           const DecodeArgs& a, int seq, int kvh, int col,
-                                          int blk) {
+                                          int blk, int hs = 0) {
   constexpr int NCH = D / 32;
   constexpr int GPL = 4 / NG;
+  constexpr bool K8 = KCH == 2 * NCH;
   const int G = a.group;
-  const int gs = a.kp.group_size;
-  const int rows = G * NG;
+  const int nh = min(heads_per_set<NG>(), G - hs);
+  // rows (g, kg): kg is a K scale group for INT4 K; for INT8 K the NG row
+  // groups split the head dim in equal parts that share the K scale(s)
+  const int gs = K8 ? D / NG : a.kp.group_size;
+  const int rows = nh * NG;
   // ---- masked q (row r = col): this lane's D/4 consecutive elements ----------
   float qpart = 0.0f;
   {
     const int r = col;
     const int g = r < rows ? r / NG : 0;
     const bool on = r < rows && ((D / 4) * blk) / gs == r % NG;
-    const uint16_t* qp = a.q + seq * a.q_stride_seq + (kvh * G + g) * a.q_stride_head + (D / 4) * blk;
+    const uint16_t* qp =
+        a.q + seq * a.q_stride_seq + (kvh * G + hs + g) * a.q_stride_head + (D / 4) * blk;
     uint16_t qv[D / 4];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
@@ -511,11 +568,12 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W
     for (int c = 0; c < NCH; ++c) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const _Float16 v = on ? __builtin_bit_cast(_Float16, qv[8 * c + kNibK[e]]) : _Float16(0);
+        const int el = 8 * c + (K8 ? kByteK8[e] : kNibK[e]);
+        const _Float16 v = on ? __builtin_bit_cast(_Float16, qv[el]) : _Float16(0);
         // odd nibbles arrive as 16 n: their q slot holds q / 16 (exact
         // unless |q| < 2^-10, where the fp16 subnormal keeps an absolute
-        // error below 2^-25)
-        W.aq[c][e] = (e & 2) ? v * static_cast<_Float16>(0.0625f) : v;
+        // error below 2^-25); INT8 codes arrive as n + 128
+        W.aq[c][e] = (!K8 && (e & 2)) ? v * static_cast<_Float16>(0.0625f) : v;
         qpart += static_cast<float>(v);
       }
     }
@@ -526,7 +584,8 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W
   for (int i = 0; i < 4; ++i) {
     // 2^-24 is exact in fp32: K codes enter the QK product as n * 2^-24
     W.qsum24[i] = __shfl(qpart, 4 * blk + i, kWave) * 0x1p-24f;
-    if constexpr (!KASYM) W.cinit[i] = -8.0f * W.qsum24[i];
+    if constexpr (K8) W.cinit[i] = -128.0f * W.qsum24[i];
+    else if constexpr (!KASYM) W.cinit[i] = -8.0f * W.qsum24[i];
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.eye[e] = (blk == col / 4 && e == col % 4) ? 1.0f : 0.0f;
@@ -548,19 +607,20 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM>& W
 
 // Reduce over tokens and write the wave's partial (acc, max, sum).  COLS:
 // the accumulators follow pv_columns' column order, else pv_transposed's.
-template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false>
-__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM>& W,
+template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false, int KCH = D / 32,
+          int NGK = NG>
+__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK>& W,
                                                const DecodeArgs& a, int seq, int kvh,
-                                               int split, int col, int blk) {
+                                               int split, int col, int blk, int hs = 0) {
   constexpr int NCH = D / 32;
   constexpr int GPL = 4 / NG;
-  const int G = a.group;
-  const int gs = a.kp.group_size;
+  const int G = min(heads_per_set<NG>(), a.group - hs);   // heads of this set
+  const int gs = a.vp.group_size;
 #pragma unroll
   for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]);
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.zacc[e] = row_sum16(W.zacc[e]);
-  const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * G;
+  const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * a.group + hs;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
 #pragma unroll
@@ -680,65 +740,90 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
 
 // ---------------------------------------------------------------------------
 // Cooperative page staging, for caches whose kv heads are densely packed in a
-// token row (stride_head = D/2 code bytes and D/G scales) and Hkv % 8 == 0.
+// token row (stride_head = one head's code bytes and scale halves) and
+// Hkv % 8 == 0.
 //
 // A block is 8 waves serving 8 consecutive kv heads of one (sequence, split),
 // so each 16-token sub-tile of each array (codes K and V, scales and zeros) is
 // 16 rows of 8 heads' contiguous bytes.  The block copies a 32-token tile
-// from HBM straight into LDS with buffer_load ... lds (16 bytes per lane, one
-// wave instruction = 1 KB of consecutive rows), one tile ahead of the
+// from HBM straight into LDS with global_load_lds (16 bytes per lane, one
+// wave instruction = 1 KB of consecutive rows), NBUF - 1 tiles ahead of the
 // compute; after a barrier each wave reads its own head's slice in the lane
 // layout of the per-head kernel.  Per-head loads touch 64-byte fragments at a
 // 512-byte stride and 8-byte scale fragments at a 64-byte stride, which
-// measured 55-59% of HBM peak even without compute; page-contiguous loads
-// measured 82-85%, as fast as a plain stream.  The direct-to-LDS copy keeps
-// the staging out of VGPRs, so two blocks (16 waves) fit on a CU.
+// measured 55-59% of HBM peak even without compute; page-contiguous copies
+// run as fast as a plain stream.  The direct-to-LDS copy keeps the staging
+// out of VGPRs.
+//
+// K is packed INT4 (NG scale groups, the same as V's) or INT8 (one byte per
+// element, NGK scale groups: 1 for one scale per row, or NG).  A wave serves
+// the G query heads of its kv head in head sets of 16 / NG heads, one
+// WaveState each (G = 5 with g32 V: heads 0-3 and head 4); the sets share the
+// staged tile and, after common-subexpression elimination, its K and V
+// conversions.
 // ---------------------------------------------------------------------------
-template <int D, int NG>
+template <int D, int NG, bool K8 = false, int NGK = NG>
 struct CoopLayout {
   static constexpr int kHeads = 8;
-  static constexpr int HB = D / 2;                // code bytes per head and token
-  static constexpr int SB = 2 * NG;               // scale bytes per head and token
-  static constexpr int CROW = kHeads * HB;        // LDS row of codes (16 rows per sub-tile)
-  static constexpr int SROW = kHeads * SB;        // LDS row of one scale array
-  static constexpr int CPS = 16 * CROW / 1024;    // 1-KB wave copies per code sub-tile
-  static constexpr int NJ = 2 * 2 * CPS / 8;      // code copies per wave and tile
-  static constexpr int NPW = NJ / 2;              // code parts per wave, array and tile
+  static constexpr int HBK = K8 ? D : D / 2;       // K code bytes per head and token
+  static constexpr int HBV = D / 2;                // V code bytes per head and token
+  static constexpr int SBK = 2 * NGK;              // K scale bytes per head and token
+  static constexpr int SBV = 2 * NG;               // V scale bytes per head and token
+  static constexpr int CROWK = kHeads * HBK;       // LDS rows (16 rows per sub-tile)
+  static constexpr int CROWV = kHeads * HBV;
+  static constexpr int SROWK = kHeads * SBK;
+  static constexpr int SROWV = kHeads * SBV;
+  static constexpr int CPSK = 16 * CROWK / 1024;   // 1-KB wave copies per code sub-tile
+  static constexpr int CPSV = 16 * CROWV / 1024;
+  static constexpr int NPWK = CPSK / 4;            // code parts per wave and tile (4 waves
+  static constexpr int NPWV = CPSV / 4;            // per sub-tile)
+  static constexpr int NJ = NPWK + NPWV;           // code copies per wave and tile
+  static constexpr bool HAS_KZ = !K8;              // K zero-points (asymmetric INT4 K)
   static constexpr int K_OFF = 0;
-  static constexpr int V_OFF = 2 * 16 * CROW;
-  static constexpr int S_OFF = 4 * 16 * CROW;     // 4 arrays (ks, vs, kz, vz) x 2 sub-tiles
-  static constexpr int BYTES = S_OFF + 8 * 16 * SROW;
-  static_assert(CPS % 4 == 0 && NPW >= 1 && NPW <= 2,
+  static constexpr int V_OFF = K_OFF + 2 * 16 * CROWK;
+  static constexpr int KS_OFF = V_OFF + 2 * 16 * CROWV;   // scale arrays, 2 sub-tiles each
+  static constexpr int VS_OFF = KS_OFF + 2 * 16 * SROWK;
+  static constexpr int KZ_OFF = VS_OFF + 2 * 16 * SROWV;
+  static constexpr int VZ_OFF = KZ_OFF + (HAS_KZ ? 2 * 16 * SROWK : 0);
+  static constexpr int BYTES = VZ_OFF + 2 * 16 * SROWV;
+  // LDS tile buffers at one block per CU (160 KB): copies run NBUF - 1 tiles ahead
+  static constexpr int NBUF = 4 * BYTES <= 160 * 1024 ? 4 : 3 * BYTES <= 160 * 1024 ? 3 : 2;
+  static_assert(NBUF * BYTES <= 160 * 1024, "tile buffers fit one CU's LDS");
+  static_assert(CPSK % 4 == 0 && CPSV % 4 == 0 && NPWK >= 1 && NPWK <= 4 && NPWV <= 2,
                 "each sub-tile's code parts split evenly over its 4 waves");
-  static_assert(16 * SROW <= 1024, "one wave copy per scale sub-tile");
-  // Rows are not padded; bank conflicts are avoided by XOR swizzles, so two
-  // blocks' double buffers fit one CU's LDS.  The 16-byte chunk c of code
-  // row r (r < 16) lives at chunk c ^ r: the 16 rows a wave reads at one head
-  // offset then cover all 64 banks.
-  __host__ __device__ static constexpr int code_off(int r, int byte) {
-    return r * CROW + ((((byte >> 4) ^ r) << 4) | (byte & 15));
+  static_assert(16 * SROWK <= 1024 && 16 * SROWV <= 1024, "one wave copy per scale sub-tile");
+  // scale array a: 0 K scales, 1 V scales, 2 K zeros, 3 V zeros
+  __host__ __device__ static constexpr int s_off(int a) {
+    return a == 0 ? KS_OFF : a == 1 ? VS_OFF : a == 2 ? KZ_OFF : VZ_OFF;
+  }
+  __host__ __device__ static constexpr int s_row(int a) { return (a & 1) ? SROWV : SROWK; }
+  // Rows are not padded; bank conflicts are avoided by XOR swizzles.  The
+  // 16-byte chunk c of code row r (r < 16) lives at chunk c ^ r: the 16 rows a
+  // wave reads at one head offset then cover all 64 banks.
+  __host__ __device__ static constexpr int code_off(int crow, int r, int byte) {
+    return r * crow + ((((byte >> 4) ^ r) << 4) | (byte & 15));
   }
   // The 16-byte chunk c of scale row r lives at chunk c ^ scale_swz(r); the
   // 16 rows' slots of one head then fall in distinct banks.
-  __host__ __device__ static constexpr int scale_swz(int r) {
-    return SROW >= 32 ? (r * SROW / 256) & (SROW / 16 - 1) : 0;
+  __host__ __device__ static constexpr int scale_swz(int srow, int r) {
+    return srow >= 32 ? (r * srow / 256) & (srow / 16 - 1) : 0;
   }
-  __host__ __device__ static constexpr int scale_off(int r, int byte) {
-    return r * SROW + ((((byte >> 4) ^ scale_swz(r)) << 4) | (byte & 15));
+  __host__ __device__ static constexpr int scale_off(int srow, int r, int byte) {
+    return r * srow + ((((byte >> 4) ^ scale_swz(srow, r)) << 4) | (byte & 15));
   }
 };
 
 // Loop-invariant addressing of the cooperative copy.  Strides are in bytes
 // and fit 32 bits (the host checks), so a page's address is one 32x32->64
 // multiply-add on the scalar unit.  Wave w copies sub-tile x = w % 2 only:
-// code parts w / 2 (+ 4) of K and V and the scale chunk of array w / 2, so
+// code parts w / 2 + 4k of K and V and the scale chunk of array w / 2, so
 // each wave looks up one page per tile.
 struct CoopAddr {
   const uint8_t* kc;      // codes of head h0 (block/page strides below)
   const uint8_t* vc;
   const uint8_t* sp;      // this wave's scale array, head h0
   uint32_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
-  uint32_t lk[2], lv[2], ls;   // lane byte offsets in HBM (code parts, scale chunk)
+  uint32_t lk[4], lv[2], ls;   // lane byte offsets in HBM (code parts, scale chunk)
   bool same_kv;           // K and V codes share their strides (one page offset)
   bool s_arr_on;          // this wave copies a scale array (wave-uniform)
   bool s_on;              // this lane copies a scale chunk
@@ -747,9 +832,6 @@ struct CoopAddr {
   const int32_t* bt;
   int bs_shift;
 };
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
 
 // 16 bytes per lane from global memory (64-bit scalar base + 32-bit lane
 // offset) straight into LDS at m0 + 16 * lane.
@@ -779,21 +861,21 @@ __device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, cons
 // at all, except when the window moves on (every 64 pages), whose refill
 // waits for its own load inside the refill.  A second half wholly past the
 // end re-reads the first half's page (its tokens are masked).
-template <int D, int NG>
+template <class L>
 __device__ __forceinline__ void coop_issue(const CoopAddr& C, PageWindow& PW, int lane,
                                            int wave, int tb, int t_end, uint8_t* buf) {
-  using L = CoopLayout<D, NG>;
   const int pb = (C.x == 0 || tb + 16 < t_end) ? tb + 16 * C.x : tb;
   const uint32_t pg = static_cast<uint32_t>(PW.page(C.bt, lane, pb >> C.bs_shift));
   const uint32_t of = static_cast<uint32_t>(pb & ((1 << C.bs_shift) - 1));
   const uint64_t ok = static_cast<uint64_t>(pg) * C.kc_b + of * C.kc_p;
   const uint64_t ov = C.same_kv ? ok : static_cast<uint64_t>(pg) * C.vc_b + of * C.vc_p;
-  uint8_t* dst = buf + C.x * 16 * L::CROW + (wave >> 1) * 1024;
+  const int p0 = (wave >> 1) * 1024;
+  uint8_t* dk = buf + L::K_OFF + C.x * 16 * L::CROWK + p0;
+  uint8_t* dv = buf + L::V_OFF + C.x * 16 * L::CROWV + p0;
 #pragma unroll
-  for (int k = 0; k < L::NPW; ++k) {
-    lds_copy16(C.kc + ok, C.lk[k], dst + L::K_OFF + k * 4096);
-    lds_copy16(C.vc + ov, C.lv[k], dst + L::V_OFF + k * 4096);
-  }
+  for (int k = 0; k < L::NPWK; ++k) lds_copy16(C.kc + ok, C.lk[k], dk + k * 4096);
+#pragma unroll
+  for (int k = 0; k < L::NPWV; ++k) lds_copy16(C.vc + ov, C.lv[k], dv + k * 4096);
   if (C.s_arr_on) {
     const uint64_t os = static_cast<uint64_t>(pg) * C.sp_b + of * C.sp_p;
     if (C.s_on) lds_copy16(C.sp + os, C.ls, buf + C.s_lds);
@@ -832,24 +914,35 @@ __device__ __forceinline__ void halves_from_lds(Halves<NG>& h, const uint8_t* p)
     h.v = *reinterpret_cast<const uint16_t*>(p);
 }
 
-// This wave's head slice of the tile in `buf`, in the per-head lane layout.
-template <int D, int NG, bool KASYM, bool VASYM>
+// This wave's head slice of the tile in `buf`, in the per-head lane layout:
+// each lane holds a quarter of its token's K row (D/8 bytes of INT4 codes or
+// D/4 bytes of INT8 codes) and the token's scale / zero halves.
+template <class L, bool KASYM, bool VASYM, int NCH, int NG, int KCH, int NGK>
 __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col, int blk,
-                                          SubTile<D / 32, NG> (&st)[2]) {
-  using L = CoopLayout<D, NG>;
-  constexpr int LB = D / 8;
+                                          SubTile<NCH, NG, KCH, NGK> (&st)[2]) {
+  constexpr int KLB = L::HBK / 4;    // K code bytes per lane and token
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    const int co = x * 16 * L::CROW + L::code_off(col, wave * L::HB + blk * LB);
-    if constexpr (D == 128)
-      st[x].k.v = *reinterpret_cast<const uint4*>(buf + L::K_OFF + co);
-    else
-      st[x].k.v = *reinterpret_cast<const uint2*>(buf + L::K_OFF + co);
-    const int so = L::S_OFF + x * 16 * L::SROW + L::scale_off(col, wave * L::SB);
-    halves_from_lds<NG>(st[x].ks, buf + so);
-    halves_from_lds<NG>(st[x].vs, buf + so + 1 * 2 * 16 * L::SROW);
-    if constexpr (KASYM) halves_from_lds<NG>(st[x].kz, buf + so + 2 * 2 * 16 * L::SROW);
-    if constexpr (VASYM) halves_from_lds<NG>(st[x].vz, buf + so + 3 * 2 * 16 * L::SROW);
+    const uint8_t* kp = buf + L::K_OFF + x * 16 * L::CROWK;
+    const int kb = wave * L::HBK + blk * KLB;
+    if constexpr (KLB == 32) {
+      st[x].k.v = *reinterpret_cast<const uint4*>(kp + L::code_off(L::CROWK, col, kb));
+      st[x].k.w = *reinterpret_cast<const uint4*>(kp + L::code_off(L::CROWK, col, kb + 16));
+    } else if constexpr (KLB == 16) {
+      st[x].k.v = *reinterpret_cast<const uint4*>(kp + L::code_off(L::CROWK, col, kb));
+    } else {
+      st[x].k.v = *reinterpret_cast<const uint2*>(kp + L::code_off(L::CROWK, col, kb));
+    }
+    halves_from_lds<NGK>(st[x].ks, buf + L::KS_OFF + x * 16 * L::SROWK +
+                                       L::scale_off(L::SROWK, col, wave * L::SBK));
+    halves_from_lds<NG>(st[x].vs, buf + L::VS_OFF + x * 16 * L::SROWV +
+                                      L::scale_off(L::SROWV, col, wave * L::SBV));
+    if constexpr (KASYM)
+      halves_from_lds<NG>(st[x].kz, buf + L::KZ_OFF + x * 16 * L::SROWK +
+                                        L::scale_off(L::SROWK, col, wave * L::SBK));
+    if constexpr (VASYM)
+      halves_from_lds<NG>(st[x].vz, buf + L::VZ_OFF + x * 16 * L::SROWV +
+                                        L::scale_off(L::SROWV, col, wave * L::SBV));
   }
 }
 
@@ -857,16 +950,15 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
 // D/32 bytes at columns (D/16)*col.. of token 16x + 4blk + i.  The four lane
 // blocks read rows 4blk + i, whose chunk swizzles differ, so the 64 lanes
 // hit 64 distinct banks.
-template <int D, int NG>
+template <class L, int D>
 __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int col, int blk,
                                             uint32_t (&vw)[2][4]) {
-  using L = CoopLayout<D, NG>;
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int o = L::V_OFF + x * 16 * L::CROW +
-                    L::code_off(4 * blk + i, wave * L::HB + (D / 32) * col);
+      const int o = L::V_OFF + x * 16 * L::CROWV +
+                    L::code_off(L::CROWV, 4 * blk + i, wave * L::HBV + (D / 32) * col);
       if constexpr (D == 128)
         vw[x][i] = *reinterpret_cast<const uint32_t*>(buf + o);
       else
@@ -879,45 +971,58 @@ __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int co
 // slice of tile i from `cur`, then QK and scores of tile i next to PV of tile
 // i - 1 (independent work for the matrix cores while the VALU converts and
 // scales), tile i's V into the registers that PV has just consumed, the
-// running-max update, and P' of tile i, which PV consumes in the next call.  Ends with a wait for this wave's copies of tile i + 1 and
-// a block barrier, after which every wave's copies of tile i + 1 have landed.
-template <int D, int NG, bool KASYM, bool VASYM, int NBUF, bool MASK, bool PV_PREV>
-__device__ __forceinline__ void coop_tile(WaveState<D / 32, NG, KASYM, VASYM>& W,
-                                          const CoopAddr& C, int i, int ntiles, int t_begin,
-                                          int t_end, int wave, int col, int blk,
+// running-max update, and P' of tile i, which PV consumes in the next call.
+// Every head set runs the same steps on the same staged data.  Ends with a
+// wait for this wave's copies of tile i + 1 and a block barrier, after which
+// every wave's copies of tile i + 1 have landed.
+template <class L, int D, int NSET, bool MASK, bool PV_PREV, class WS>
+__device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int i, int ntiles,
+                                          int t_begin, int t_end, int wave, int col, int blk,
                                           const uint8_t* cur, uint8_t* nxt, uint32_t (&vw)[2][4],
-                                          h8& ahi, h8& alo, PageWindow& PW, int lane) {
-  constexpr int NCH = D / 32;
+                                          h8 (&ahi)[NSET], h8 (&alo)[NSET], PageWindow& PW,
+                                          int lane) {
+  constexpr int NBUF = L::NBUF;
   const int tb = t_begin + 32 * i;
   // `nxt` was last read by tile i - 1, before the previous barrier
-  if (i + NBUF - 1 < ntiles) coop_issue<D, NG>(C, PW, lane, wave, tb + 32 * (NBUF - 1), t_end, nxt);
-  SubTile<NCH, NG> st[2];
-  coop_read<D, NG, KASYM, VASYM>(cur, wave, col, blk, st);
+  if (i + NBUF - 1 < ntiles) coop_issue<L>(C, PW, lane, wave, tb + 32 * (NBUF - 1), t_end, nxt);
+  typename WS::ST st[2];
+  coop_read<L, WS::KZ_USED, WS::VZ_USED>(cur, wave, col, blk, st);
   bool valid[2] = {true, true};
   if constexpr (MASK) {
     valid[0] = tb + col < t_end;
     valid[1] = tb + 16 + col < t_end;
   }
-  float score[2][4 / NG];
-  W.template scores<MASK>(st, valid, score);
-  if constexpr (PV_PREV) W.pv_columns(vw, ahi, alo);
+  float score[NSET][2][WS::GPL];
+#pragma unroll
+  for (int s = 0; s < NSET; ++s) W[s].template scores<MASK>(st, valid, score[s]);
+  if constexpr (PV_PREV) {
+#pragma unroll
+    for (int s = 0; s < NSET; ++s) W[s].pv_columns(vw, ahi[s], alo[s]);
+  }
   // tile i's V replaces tile i - 1's in place once its PV has consumed it
-  coop_read_v<D, NG>(cur, wave, col, blk, vw);
-  if (W.max_moves(score)) W.raise_max(score);
-  W.template probs<MASK>(st, valid, score, ahi, alo);
+  coop_read_v<L, D>(cur, wave, col, blk, vw);
+#pragma unroll
+  for (int s = 0; s < NSET; ++s) {
+    if (W[s].max_moves(score[s])) W[s].raise_max(score[s]);
+    W[s].template probs<MASK>(st, valid, score[s], ahi[s], alo[s]);
+  }
   // copies issued after tile i + 1's: tiles i + 2 .. min(i + NBUF - 1, ntiles - 1)
-  wait_tile_copies<CoopLayout<D, NG>::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
+  wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
   __syncthreads();
 }
 
-// One block per CU (8 waves), NBUF tile buffers of LDS: the copies run
-// NBUF - 1 tiles ahead of the compute.
-template <int D, int NG, bool KASYM, bool VASYM, int NBUF>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(NBUF == 2 ? 4 : 2)))
+// One block per CU (8 waves), L::NBUF tile buffers of LDS: the copies run
+// NBUF - 1 tiles ahead of the compute.  K8: INT8 K codes with NGK scale
+// groups; NSET head sets per wave.
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_mfma_coop_kernel(DecodeArgs a) {
-  using L = CoopLayout<D, NG>;
+  using L = CoopLayout<D, NG, K8, NGK>;
   constexpr int NCH = D / 32;
-  static_assert(NBUF >= 2 && NBUF <= 4, "copies one to three tiles ahead");
+  constexpr int KCH = K8 ? 2 * NCH : NCH;
+  constexpr int NBUF = L::NBUF;
+  using WS = WaveState<NCH, NG, KASYM, VASYM, KCH, NGK>;
+  static_assert(!(K8 && KASYM), "INT8 K is symmetric");
   __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][L::BYTES];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -938,8 +1043,11 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   decode_append<D>(a, seq, kvh, split, seq_len, lane);
   if (a.app.key != nullptr || a.app.value != nullptr) __syncthreads();
 
-  WaveState<NCH, NG, KASYM, VASYM> W;
-  init_wave<D, NG, KASYM, VASYM>(W, a, seq, kvh, col, blk);
+  WS W[NSET];
+#pragma unroll
+  for (int s = 0; s < NSET; ++s)
+    init_wave<D, NG, KASYM, VASYM, KCH, NGK>(W[s], a, seq, kvh, col, blk,
+                                             s * heads_per_set<NG>());
 
   CoopAddr C;
   {
@@ -955,11 +1063,17 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     // code copy: lane -> LDS byte part*1024 + 16*lane of a sub-tile, which
     // holds logical chunk (physical chunk) ^ row of that row
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int byte = ((wave >> 1) + 4 * k) % L::CPS * 1024 + 16 * lane;
-      const int r = byte / L::CROW;
-      const int c = ((byte % L::CROW) >> 4) ^ r;
+    for (int k = 0; k < 4; ++k) {
+      const int byte = ((wave >> 1) + 4 * k) % L::CPSK * 1024 + 16 * lane;
+      const int r = byte / L::CROWK;
+      const int c = ((byte % L::CROWK) >> 4) ^ r;
       C.lk[k] = static_cast<uint32_t>(r * K.stride_page + 16 * c);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int byte = ((wave >> 1) + 4 * k) % L::CPSV * 1024 + 16 * lane;
+      const int r = byte / L::CROWV;
+      const int c = ((byte % L::CROWV) >> 4) ^ r;
       C.lv[k] = static_cast<uint32_t>(r * V.stride_page + 16 * c);
     }
     // wave w copies scale array w / 2 (ks, vs, kz, vz) of sub-tile w % 2
@@ -976,18 +1090,19 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     const int64_t spg = arr == 0 ? K.s_stride_page : arr == 1 ? V.s_stride_page
                       : arr == 2 ? K.z_stride_page : V.z_stride_page;
     const bool arr_on = arr < 2 || (arr == 2 && KASYM) || (arr == 3 && VASYM);
+    const int srow = L::s_row(arr);
     C.s_arr_on = arr_on;
-    C.s_on = arr_on && 16 * lane < 16 * L::SROW;
+    C.s_on = arr_on && lane < srow;
     C.sp = arr_on ? reinterpret_cast<const uint8_t*>(base + h0 * sh) : nullptr;
     C.sp_b = static_cast<uint32_t>(2 * sbk);
     C.sp_p = static_cast<uint32_t>(2 * spg);
     {
       const int byte = 16 * lane;
-      const int r = byte / L::SROW;
-      const int c = ((byte % L::SROW) >> 4) ^ L::scale_swz(r);
+      const int r = byte / srow;
+      const int c = ((byte % srow) >> 4) ^ L::scale_swz(srow, r);
       C.ls = static_cast<uint32_t>(r * C.sp_p + 16 * c);
     }
-    C.s_lds = L::S_OFF + (arr * 2 + C.x) * 16 * L::SROW;
+    C.s_lds = L::s_off(arr) + C.x * 16 * srow;
     C.bt = a.block_table + seq * a.bt_stride;
     C.bs_shift = a.block_shift;
   }
@@ -998,19 +1113,18 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   PW.fill(C.bt, lane, t_begin >> C.bs_shift);
 #pragma unroll
   for (int t = 0; t < NBUF - 1; ++t)
-    if (t < ntiles)
-      coop_issue<D, NG>(C, PW, lane, wave, t_begin + 32 * t, t_end, lds[t]);
+    if (t < ntiles) coop_issue<L>(C, PW, lane, wave, t_begin + 32 * t, t_end, lds[t]);
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
   // the PV of the last tile
   uint32_t vw[2][4];
-  h8 ahi, alo;
+  h8 ahi[NSET], alo[NSET];
   const int nfull = (t_end - t_begin) / 32;
-#define KNLP_COOP_TILE(MASK, PV_PREV)                                                     \
-  coop_tile<D, NG, KASYM, VASYM, NBUF, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, \
-                                                      col, blk, lds[i % NBUF],            \
-                                                      lds[(i + NBUF - 1) % NBUF], vw, ahi, alo, PW, lane)
+#define KNLP_COOP_TILE(MASK, PV_PREV)                                                       \
+  coop_tile<L, D, NSET, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, col, blk,     \
+                                       lds[i % NBUF], lds[(i + NBUF - 1) % NBUF], vw, ahi,  \
+                                       alo, PW, lane)
   int i = 0;
   if (nfull > 0) {
     KNLP_COOP_TILE(false, false);
@@ -1020,8 +1134,12 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     KNLP_COOP_TILE(true, false);
   }
 #undef KNLP_COOP_TILE
-  W.pv_columns(vw, ahi, alo);
-  write_partials<D, NG, KASYM, VASYM, true>(W, a, seq, kvh, split, col, blk);
+#pragma unroll
+  for (int s = 0; s < NSET; ++s) {
+    W[s].pv_columns(vw, ahi[s], alo[s]);
+    write_partials<D, NG, KASYM, VASYM, true, KCH, NGK>(W[s], a, seq, kvh, split, col, blk,
+                                                        s * heads_per_set<NG>());
+  }
 }
 
 int heads_per_block_mfma(int num_kv_heads) {
@@ -1032,24 +1150,37 @@ int heads_per_block_mfma(int num_kv_heads) {
 
 }  // namespace
 
+// Shapes the matrix-core path takes: INT4 V with 1, 2 or 4 scale groups,
+// fp16 q, D = 64 or 128, K packed INT4 with V's groups or (D = 128) INT8 with
+// one scale per row or V's groups, and at most two head sets of 16 rows.  The
+// per-head kernel covers INT4 K with one head set; the other shapes need the
+// cooperative kernel's dense layout and otherwise run on the VALU kernel.
 bool mfma_supported(int group, int head_size, int k_format, int k_gs, int v_format, int v_gs,
                     int q_bf16) {
-  const bool int4 = (k_format == KNLP_KV_INT4_SYM || k_format == KNLP_KV_INT4_ASYM) &&
-                    (v_format == KNLP_KV_INT4_SYM || v_format == KNLP_KV_INT4_ASYM);
-  if (!int4 || q_bf16 || k_gs != v_gs || k_gs <= 0) return false;
+  const auto int4 = [](int f) { return f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM; };
+  if (!int4(v_format) || q_bf16 || v_gs <= 0) return false;
   if (head_size != 64 && head_size != 128) return false;
-  const int ng = head_size / k_gs;
+  if (head_size % v_gs) return false;
+  const int ng = head_size / v_gs;
   if (ng != 1 && ng != 2 && ng != 4) return false;
-  return group >= 1 && group * ng <= 16;
+  if (int4(k_format)) {
+    if (k_gs != v_gs) return false;
+  } else if (k_format == KNLP_KV_INT8_SYM) {
+    if (head_size != 128 || (k_gs != head_size && k_gs != v_gs)) return false;
+  } else {
+    return false;
+  }
+  return group >= 1 && group * ng <= 32;
 }
 
 // Heads densely packed in a token row, 16-byte aligned rows, Hkv % 8 == 0:
 // the cooperative kernel can fetch 8 heads' rows as one contiguous run.
 static bool coop_layout_ok(const knlp_kv_plane& P, int head_size, int num_kv_heads) {
   const int64_t ng = head_size / P.group_size;
+  const int64_t row = P.format == KNLP_KV_INT8_SYM ? head_size : head_size / 2;
   const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   if (num_kv_heads % 8 != 0) return false;
-  if (!a16(P.data) || P.stride_head != head_size / 2 || P.stride_block % 16 != 0 ||
+  if (!a16(P.data) || P.stride_head != row || P.stride_block % 16 != 0 ||
       P.stride_page % 16 != 0 || P.stride_block >= (1LL << 31) || P.stride_page >= (1LL << 31))
     return false;
   const auto scales_ok = [&](const void* p, int64_t sb, int64_t sp, int64_t sh) {
@@ -1064,40 +1195,68 @@ static bool coop_layout_ok(const knlp_kv_plane& P, int head_size, int num_kv_hea
 }
 
 int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
-  const int ng = head_size / a.kp.group_size;
+  const int ng = head_size / a.vp.group_size;
+  const bool k8 = a.kp.format == KNLP_KV_INT8_SYM;
+  const int ngk = head_size / a.kp.group_size;
   const bool ka = a.kp.format == KNLP_KV_INT4_ASYM;
   const bool va = a.vp.format == KNLP_KV_INT4_ASYM;
+  const int nset = (a.group * ng + 15) / 16;
   const bool coop = coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
                     coop_layout_ok(a.vp, head_size, a.num_kv_heads);
+  if (!coop && (k8 || nset > 1))     // only the cooperative kernel has these
+    return launch_decode_valu(a, head_size, heads_per_block_mfma(a.num_kv_heads), stream);
   const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
   const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
   const dim3 block(kWave * hpb);
-#define KNLP_MFMA_K(KERNEL, D, NG, ...)                                                  \
-  if (ka && va)                                                                          \
-    hipLaunchKernelGGL((KERNEL<D, NG, true, true __VA_ARGS__>), grid, block, 0, stream, a);  \
-  else if (ka)                                                                           \
-    hipLaunchKernelGGL((KERNEL<D, NG, true, false __VA_ARGS__>), grid, block, 0, stream, a); \
-  else if (va)                                                                           \
-    hipLaunchKernelGGL((KERNEL<D, NG, false, true __VA_ARGS__>), grid, block, 0, stream, a); \
-  else                                                                                   \
-    hipLaunchKernelGGL((KERNEL<D, NG, false, false __VA_ARGS__>), grid, block, 0, stream, a);
-#define KNLP_MFMA(D, NG)                                                                 \
-  if (head_size == D && ng == NG) {                                                      \
-    if (coop) {                                                                          \
-      KNLP_MFMA_K(decode_mfma_coop_kernel, D, NG, , 4)                                   \
-    } else {                                                                             \
-      KNLP_MFMA_K(decode_mfma_kernel, D, NG)                                             \
-    }                                                                                    \
-    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                  \
+#define KNLP_LAUNCH(...)                                                                 \
+  hipLaunchKernelGGL((__VA_ARGS__), grid, block, 0, stream, a)
+#define KNLP_ASYM(KERNEL, D, NG, ...)                                                     \
+  if (ka && va) KNLP_LAUNCH(KERNEL<D, NG, true, true __VA_ARGS__>);                       \
+  else if (ka) KNLP_LAUNCH(KERNEL<D, NG, true, false __VA_ARGS__>);                       \
+  else if (va) KNLP_LAUNCH(KERNEL<D, NG, false, true __VA_ARGS__>);                       \
+  else KNLP_LAUNCH(KERNEL<D, NG, false, false __VA_ARGS__>);
+#define KNLP_INT4(D, NG)                                                                  \
+  if (!k8 && head_size == D && ng == NG) {                                                \
+    if (coop && nset == 1) {                                                              \
+      KNLP_ASYM(decode_mfma_coop_kernel, D, NG, , false, NG, 1)                           \
+    } else if (coop) {                                                                    \
+      KNLP_ASYM(decode_mfma_coop_kernel, D, NG, , false, NG, 2)                           \
+    } else {                                                                              \
+      KNLP_ASYM(decode_mfma_kernel, D, NG)                                                \
+    }                                                                                     \
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                   \
   }
-  KNLP_MFMA(128, 4)
-  KNLP_MFMA(128, 2)
-  KNLP_MFMA(128, 1)
-  KNLP_MFMA(64, 4)
-  KNLP_MFMA(64, 2)
-  KNLP_MFMA(64, 1)
-#undef KNLP_MFMA
-#undef KNLP_MFMA_K
+#define KNLP_INT8K_SETS(NG, NGK)                                                          \
+  if (nset == 1) {                                                                        \
+    if (va) KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, true, true, NGK, 1>);     \
+    else KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, false, true, NGK, 1>);       \
+  } else {                                                                                \
+    if (va) KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, true, true, NGK, 2>);     \
+    else KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, false, true, NGK, 2>);       \
+  }
+#define KNLP_INT8K(NG)                                                                    \
+  if (k8 && head_size == 128 && ng == NG) {                                               \
+    if (ngk == 1) {                                                                       \
+      KNLP_INT8K_SETS(NG, 1)                                                              \
+    } else {                                                                              \
+      KNLP_INT8K_SETS(NG, NG)                                                             \
+    }                                                                                     \
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                   \
+  }
+  KNLP_INT4(128, 4)
+  KNLP_INT4(128, 2)
+  KNLP_INT4(128, 1)
+  KNLP_INT4(64, 4)
+  KNLP_INT4(64, 2)
+  KNLP_INT4(64, 1)
+  KNLP_INT8K(4)
+  KNLP_INT8K(2)
+  KNLP_INT8K(1)
+#undef KNLP_INT8K
+#undef KNLP_INT8K_SETS
+#undef KNLP_INT4
+#undef KNLP_ASYM
+#undef KNLP_LAUNCH
   return KNLP_ERR_SHAPE;
 }
 

@@ -107,6 +107,15 @@ CASES = [
     ("d64_hkv8_g2", [1500, 300], 16, 8, 64, 1, 1, 32, 32),
     ("g128_d128_hkv16", [700, 129], 64, 16, 128, 1, 1, 128, 128),
     ("sym_g64_hkv8", [999], 32, 8, 128, 0, 0, 64, 64),
+    # head sets (G * groups > 16 rows) and INT8 K on the cooperative kernel,
+    # and their fallbacks to the VALU kernel for non-dense layouts (Hkv % 8)
+    ("int4_g5_two_sets", [1500, 300, 33], 40, 8, 128, 1, 1, 32, 32),
+    ("int4_sym_g8_two_sets", [700], 64, 8, 128, 0, 0, 32, 32),
+    ("int4_g10_g64_two_sets", [640], 80, 8, 128, 1, 1, 64, 64),
+    ("int4_g5_hkv4_valu", [500], 20, 4, 128, 1, 1, 32, 32),
+    ("kint8_row_vint4_g4", [777, 64], 32, 8, 128, 2, 1, 128, 32),
+    ("kint8_row_vsym_g5", [1030], 40, 8, 128, 2, 0, 128, 32),
+    ("kint8_row_hkv4_valu", [400], 20, 4, 128, 2, 1, 128, 32),
 ]
 
 
@@ -238,4 +247,13 @@ def test_kernel_kind_dispatch():
     assert kk(32, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32,
               torch.bfloat16) == "valu"
     assert kk(64, 8, 256, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "valu"
-    assert kk(40, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT4_ASYM, 32) == "valu"
+    # INT8 K (per-row or V's groups) with INT4 V, and up to two 16-row head
+    # sets, take the matrix cores when the caches are densely laid out
+    assert kk(40, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT4_ASYM, 32) == "mfma"
+    assert kk(32, 8, 128, _lib.KV_INT8_SYM, 32, _lib.KV_INT4_ASYM, 32) == "mfma"
+    assert kk(64, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "mfma"
+    with pytest.raises(ValueError):        # 9 heads x 4 groups: neither kernel
+        kk(72, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32)
+    assert kk(32, 8, 128, _lib.KV_INT8_SYM, 64, _lib.KV_INT4_ASYM, 32) == "valu"
+    assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT4_ASYM, 32) == "valu"
+    assert kk(32, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT8_SYM, 32) == "valu"
