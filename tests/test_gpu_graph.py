@@ -1,0 +1,95 @@
+"""HIP-graph capture of the decode entry points (the reference's backend
+captures its decode steps, F:2185; the library promises no allocation and no
+synchronisation inside its calls).  Each graph is replayed several times with
+eager work in between, and every replay must equal the eager result bit for
+bit."""
+import numpy as np
+import pytest
+import torch
+
+import knlp_amd as K
+from tests import kvgen
+
+pytestmark = pytest.mark.gpu
+
+BS = 16
+
+
+def _caches(seq_lens, hq, hkv, d, seed, dev):
+    nb = sum(-(-n // BS) for n in seq_lens) + 2
+    bt = kvgen.paged_table(seq_lens, BS, nb, seed)
+    planes = []
+    for i in range(2):
+        p = kvgen.empty_plane(1, nb, BS, hkv, d, 32)
+        rows = kvgen.randn((nb * BS, hkv, d), seed + 1 + i).float().numpy()
+        kvgen.fill_plane(p, rows, np.arange(nb * BS))
+        planes.append(kvgen.plane_to_torch(p, dev))
+    q = kvgen.randn((len(seq_lens), hq, d), seed + 5).to(dev)
+    return planes, torch.from_numpy(bt).to(dev), q
+
+
+@pytest.mark.parametrize("hkv", [8, 4], ids=["cooperative", "per_head"])
+def test_decode_graph_replays_match_eager(hkv):
+    dev = torch.device("cuda")
+    hq, d = 4 * hkv, 128
+    seq_lens = [1500, 77, 4096]
+    (kp, vp), bt, q = _caches(seq_lens, hq, hkv, d, 60, dev)
+    sl = torch.tensor(seq_lens, dtype=torch.int32, device=dev)
+
+    def step():
+        return K.fused_int4_decode(q, kp[0], vp[0], kp[1], vp[1], bt, sl, hkv, d,
+                                   k_zeros=kp[2], v_zeros=vp[2], asymmetric=True)
+
+    want = step()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):                 # warm the caching allocator off-graph
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got = step()
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {r}"
+        eager = step()                         # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager.view(torch.int16), want.view(torch.int16))
+
+
+def test_append_and_decode_graph():
+    """The fused append inside a captured decode: replays rewrite the same
+    token (idempotent) and return the eager output each time."""
+    dev = torch.device("cuda")
+    hq, hkv, d = 32, 8, 128
+    seq_lens = [513, 1024]
+    (kp, vp), bt, q = _caches(seq_lens, hq, hkv, d, 70, dev)
+    sl = torch.tensor(seq_lens, dtype=torch.int32, device=dev)
+    pos = np.array(seq_lens) - 1
+    btn = bt.cpu().numpy()
+    slots = torch.from_numpy(btn[np.arange(2), pos // BS].astype(np.int64) * BS + pos % BS).to(dev)
+    nk = kvgen.randn((2, hkv, d), 71).to(dev)
+    nv = kvgen.randn((2, hkv, d), 72).to(dev)
+
+    def step():
+        return K.append_and_decode(q, nk, nv, slots, kp[0], vp[0], kp[1], vp[1], bt, sl, hkv, d,
+                                   k_zeros=kp[2], v_zeros=vp[2], asymmetric=True)
+
+    want = step()
+    kc = kp[0].clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got = step()
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {r}"
+        assert torch.equal(kp[0], kc)
