@@ -193,6 +193,21 @@ int knlp_kv_append_decode(const void* query, int32_t q_dtype, int64_t q_stride_s
                           int64_t workspace_bytes, void* out, int32_t out_dtype,
                           int64_t o_stride_seq, int64_t o_stride_head, void* stream);
 
+/*
+ * Packed INT4 codes in the two's-complement nibble form of the reference's
+ * gpt2 compression path (gpt2/compression/kv_plugin.py:212-257: t in [-7, 7]
+ * stored as t & 0xF, element 2i in the low nibble) re-encoded in this
+ * library's offset form (n = t + 8, decoded as (n - 8) * scale, F:359), so
+ * such caches can be decoded as KNLP_KV_INT4_SYM planes with that path's
+ * per-row scale (group size = head size).  Byte matrix [rows, row_bytes],
+ * row_bytes % 4 == 0, row strides in bytes; dst == src converts in place.
+ * No counterpart function in the reference (its expand kernel,
+ * kernels/triton_kernels.py:62-232, sign-extends in registers instead).
+ */
+int knlp_int4_twos_to_offset(const void* src, int64_t src_stride_row, void* dst,
+                             int64_t dst_stride_row, int64_t rows, int64_t row_bytes,
+                             void* stream);
+
 /* Which decode kernel a shape dispatches to: 1 = MFMA path, 0 = VALU path,
  * negative = unsupported (status).  Lets tests and the bench report it.  The
  * MFMA path's INT8-K and more-than-16-row shapes need densely packed heads

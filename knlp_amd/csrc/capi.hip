@@ -11,6 +11,8 @@ int launch_append(const void* key, const void* value, int src_bf16, int64_t num_
                   int64_t vsh, const knlp_kv_plane& KP, const knlp_kv_plane& VP,
                   const void* slots, int slots64, int block_size, float clip_ratio,
                   hipStream_t stream);
+int launch_twos_to_offset(const void* src, int64_t src_stride, void* dst, int64_t dst_stride,
+                          int64_t rows, int64_t row_bytes, hipStream_t stream);
 }
 
 using namespace knlp;
@@ -379,6 +381,20 @@ int knlp_kv_append_decode(const void* query, int32_t q_dtype, int64_t q_stride_s
   return knlp_kv_decode_merge(workspace, workspace_bytes, seq_lens, num_seqs, num_q_heads,
                               head_size, max_context, split_tokens, out, out_dtype, o_stride_seq,
                               o_stride_head, stream);
+}
+
+int knlp_int4_twos_to_offset(const void* src, int64_t src_stride_row, void* dst,
+                             int64_t dst_stride_row, int64_t rows, int64_t row_bytes,
+                             void* stream) {
+  if (rows < 0 || row_bytes < 0 || row_bytes % 4) return KNLP_ERR_SHAPE;
+  if (rows == 0 || row_bytes == 0) return KNLP_OK;
+  if (src == nullptr || dst == nullptr) return KNLP_ERR_ARG;
+  if (!aligned(src, 4) || !aligned(dst, 4) || src_stride_row % 4 || dst_stride_row % 4)
+    return KNLP_ERR_ALIGN;
+  if ((rows > 1 && (src_stride_row < row_bytes || dst_stride_row < row_bytes)))
+    return KNLP_ERR_SHAPE;
+  return launch_twos_to_offset(src, src_stride_row, dst, dst_stride_row, rows, row_bytes,
+                               static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

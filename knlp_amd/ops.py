@@ -238,6 +238,36 @@ def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, 
     return out
 
 
+def int4_twos_to_offset(packed: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Re-encode packed INT4 codes from the gpt2 compression path's
+    two's-complement nibbles (gpt2/compression/kv_plugin.py:212-257) into
+    this library's offset nibbles (n = t + 8, F:359).  ``packed``: uint8
+    ``[..., D/2]`` with a contiguous last axis; ``out`` may be ``packed``
+    itself (in place) or None (new tensor).  With that path's per-row fp16
+    scale ``[..., 1]`` the result decodes as a symmetric INT4 plane of group
+    size D.  Not a function of the reference module."""
+    _require_cuda(packed, out)
+    if packed.dtype != torch.uint8 or packed.dim() < 1 or packed.stride(-1) != 1:
+        raise ValueError("packed must be uint8 with a contiguous last axis")
+    if out is None:
+        out = torch.empty_like(packed)
+    if out.shape != packed.shape or out.dtype != torch.uint8 or out.stride(-1) != 1:
+        raise ValueError("out must be uint8 shaped like packed, last axis contiguous")
+    rb = packed.shape[-1]
+    src2, dst2 = packed.reshape(-1, rb), out.reshape(-1, rb)
+    if dst2.data_ptr() != out.data_ptr() or (out.numel() and not _same_storage(dst2, out)):
+        raise ValueError("out must be reshapeable to rows without a copy")
+    st = lib().knlp_int4_twos_to_offset(src2.data_ptr(), src2.stride(0) if src2.dim() else rb,
+                                         dst2.data_ptr(), dst2.stride(0) if dst2.dim() else rb,
+                                         src2.shape[0], rb, _stream())
+    check(st, "knlp_int4_twos_to_offset")
+    return out
+
+
+def _same_storage(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return a.untyped_storage().data_ptr() == b.untyped_storage().data_ptr()
+
+
 _FORMATS = {"int8": KV_INT8_SYM, "fp16": KV_FP16}
 
 

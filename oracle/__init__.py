@@ -18,6 +18,10 @@ What is restated here (all references are into mcgrof/knlp,
   F:262-296 / F:418-472 / F:519-647 / F:1287-1312
 * ``attention.dequant_*``            -- ``_cpu_dequant_slot`` F:150-195 and the
   in-kernel dequantisation F:765-800, F:853-872, F:1397-1423
+* ``lineage.t5_*``                   -- the harness packer, scripts/spev01/
+  tier5_fused_decode.py:116-145 (ties to even, no clip)
+* ``lineage.gpt2_*``                 -- the gpt2 compression path's INT4 format,
+  gpt2/compression/kv_plugin.py:212-295 (two's-complement nibbles, per-row scale)
 * ``attention.decode_reference``     -- the reference's own oracle, dequantise
   then ``repeat_interleave`` then SDPA: ``scripts/v35_h100_bench.py:376-387``,
   ``scripts/v29_flash_bench.py:86-97``; output rounding of F:886-894
@@ -34,6 +38,10 @@ tests live in ``tests/test_oracle_pinning.py``):
 * reshape_and_cache_*: slot arithmetic and the slot < 0 skip against
   hand-built expectations.
 * dequant_*: closed-form groups whose dequantisation is exact.
+* lineage: closed-form rows (codes and the two's-complement bit patterns for
+  every value -7..7), agreement of the T5 packer with quantize_int4_groups
+  everywhere except at constructed .5 ties, and the identity that maps
+  the gpt2 nibbles onto this library's offset nibbles (all 256 bytes).
 * decode_reference: torch SDPA on exactly representable data, context length
   1, identical keys, GQA head equivalence, block-table permutation invariance.
 
