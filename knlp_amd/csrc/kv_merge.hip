@@ -7,15 +7,17 @@
 // bf16.  n = ceil(seq_len / split_tokens); n = 0 gives 0/0 = NaN, matching the
 // reference's acc / l_i with l_i = 0 (F:886-887).
 //
-// One block of 4 waves per (sequence, q head): wave w folds splits
-// w, w+4, ... with an online (max-rescaling) combine, then the four wave
-// states are combined through LDS.
+// One block of NW waves per (sequence, q head): wave w folds splits
+// w, w+NW, ... with an online (max-rescaling) combine, then the NW wave
+// states are combined through LDS.  NW grows with the split count (4, 8 or
+// 16 waves) so that a wave folds at most a few groups of U splits: config 4
+// (one sequence, 256 splits) merges in about a third of the time 4 waves take.
 #include "kv_decode.h"
 
 namespace knlp {
 
-template <int D>
-__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_o,
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) void merge_kernel(const float* __restrict__ part_o,
                                                     const float* __restrict__ part_ml,
                                                     const int32_t* __restrict__ seq_lens,
                                                     int hq, int max_context,
@@ -23,7 +25,6 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
                                                     void* __restrict__ out, int out_bf16,
                                                     int64_t o_stride_seq, int64_t o_stride_head) {
   constexpr int E = D >= kWave ? D / kWave : 1;     // elements per lane
-  constexpr int NW = 4;
   __shared__ float s_o[NW][D];
   __shared__ float s_m[NW], s_l[NW];
   const int h = blockIdx.x;
@@ -36,8 +37,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
 
   // Splits are taken U at a time per wave with every load of the group issued
   // before any use, so a wave waits for about one memory round trip per
-  // group instead of one per split (ns <= 32 at the benchmark shapes: one
-  // group).
+  // group instead of one per split.
   constexpr int U = 8;
   float M = -INFINITY, L = 0.0f, o[E];
 #pragma unroll
@@ -111,18 +111,26 @@ int launch_merge(const float* part_o, const float* part_ml, const int32_t* seq_l
                  void* out, int out_bf16, int64_t o_stride_seq, int64_t o_stride_head,
                  hipStream_t stream) {
   const dim3 grid(hq, num_seqs);
-  const dim3 block(256);
+  // waves per (sequence, q head): one group of U = 8 splits each up to 32
+  // splits, then 8 and 16 waves
+  const int nw = num_splits <= 32 ? 4 : num_splits <= 64 ? 8 : 16;
+  const dim3 block(kWave * nw);
   switch (head_size) {
+#define KNLP_MERGE_NW(D, NW)                                                            \
+    hipLaunchKernelGGL((merge_kernel<D, NW>), grid, block, 0, stream, part_o, part_ml,  \
+                       seq_lens, hq, max_context, split_tokens, num_splits, out, out_bf16, \
+                       o_stride_seq, o_stride_head);
 #define KNLP_MERGE_D(D)                                                                 \
   case D:                                                                               \
-    hipLaunchKernelGGL(merge_kernel<D>, grid, block, 0, stream, part_o, part_ml,        \
-                       seq_lens, hq, max_context, split_tokens, num_splits, out, out_bf16,           \
-                       o_stride_seq, o_stride_head);                                    \
+    if (nw == 4) { KNLP_MERGE_NW(D, 4) }                                                \
+    else if (nw == 8) { KNLP_MERGE_NW(D, 8) }                                           \
+    else { KNLP_MERGE_NW(D, 16) }                                                       \
     break;
     KNLP_MERGE_D(64)
     KNLP_MERGE_D(128)
     KNLP_MERGE_D(256)
 #undef KNLP_MERGE_D
+#undef KNLP_MERGE_NW
     default:
       return KNLP_ERR_SHAPE;
   }
