@@ -144,7 +144,6 @@ class Caches:
         return c
 
     def plane(self):
-        from knlp_amd._lib import KvPlane
         from knlp_amd.ops import _plane
         return _plane(self.data, self.scales, self.zeros, FMT[self.fmt], self.gs)
 

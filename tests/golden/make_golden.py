@@ -24,7 +24,6 @@ ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)
 sys.path.insert(0, ROOT)
 
 from oracle import attention as A      # noqa: E402
-from oracle import quant as Q          # noqa: E402
 from tests import kvgen                # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "int4kv_golden.npz")
