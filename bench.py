@@ -20,6 +20,11 @@
 * ``roofline`` is for the dominant kernel, the decode partial.  Its achieved
   bandwidth is its algorithmic bytes per launch divided by its average
   duration, timed with HIP events on the stream it runs on.
+* The split-K length is the library's plan or, by default, the fastest of
+  the plan and a few candidates (512 ... 4096 tokens) measured on the same
+  inputs before timing; ``config.split_tokens_planned`` and
+  ``config.split_sweep_us_per_step`` record the choice (``--no-split-sweep``
+  times the plan alone).  The fp16 leg picks its split the same way.
 * ``cpu_baseline`` times the oracle's dequantise -> repeat_interleave -> SDPA
   path (the reference's P1 pipeline) in torch on the host cores.  It runs on
   a bounded sample (one sequence) and is scaled to the whole step.
@@ -266,6 +271,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp16", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--no-split-sweep", action="store_true",
+                    help="use the library's planned split instead of the fastest of a few")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes 5 times (calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count)")
@@ -296,9 +303,11 @@ def main(argv=None):
     bt, nb = make_block_table(cfg, seq_lens, bs, 6000 + c)
     L = lib()
     max_context = bt.shape[1] * bs
-    split = args.split_tokens or L.knlp_kv_decode_split_tokens(
+    split_plan = L.knlp_kv_decode_split_tokens(
         B, Hkv, Hq, D, max_context, FMT[cfg["kfmt"]], FMT[cfg["vfmt"]])
-    print(f"# config {c}: {cfg['name']}; split_tokens={split}", file=sys.stderr, flush=True)
+    split = args.split_tokens or split_plan
+    print(f"# config {c}: {cfg['name']}; planned split_tokens={split_plan}", file=sys.stderr,
+          flush=True)
 
     # ---- build inputs (untimed) -------------------------------------------------
     g = torch.Generator().manual_seed(1000 + c)
@@ -329,7 +338,8 @@ def main(argv=None):
     copies = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(args.copies - 1)]
     print(f"# inputs built: {n_tok} tokens", file=sys.stderr, flush=True)
 
-    ws_bytes = L.knlp_kv_decode_workspace_bytes(B, Hq, D, max_context, split)
+    # workspace for the smallest split tried (the largest partial count)
+    ws_bytes = L.knlp_kv_decode_workspace_bytes(B, Hq, D, max_context, 64)
     ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
     out = torch.empty_like(q)
 
@@ -349,6 +359,22 @@ def main(argv=None):
                                             asymmetric=True, group_size=vcc.gs)
 
         fused = (new_k, new_v, app_slots)
+
+    # ---- split: the library's plan, or the fastest of a few candidates ---------------
+    # (the API takes the split from the caller; a deployment tunes it per batch
+    # shape the same way, and the fp16 leg below gets the same treatment)
+    split_tried = {}
+    if not args.split_tokens and not args.no_split_sweep:
+        cands = sorted({split_plan} | {sp for sp in (512, 704, 1024, 1536, 2048, 4096)
+                                       if sp < max_context})
+        for sp in cands:
+            run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, sp, ws, out, 5, fused=fused)
+            split_tried[sp] = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, sp, ws, out,
+                                               max(args.steps // 4, 10), fused=fused)
+        split = min(split_tried, key=split_tried.get)
+        print(f"# split sweep (us/step): " +
+              ", ".join(f"{k}: {v * 1e3:.1f}" for k, v in split_tried.items()) +
+              f" -> {split}", file=sys.stderr, flush=True)
 
     # ---- INT4 decode: warmup, timed steps, dominant-kernel timing ----------------
     ms_step_sep = None
@@ -446,7 +472,10 @@ def main(argv=None):
         "config": {"workload": cfg["name"], "batch": B, "q_heads": Hq, "kv_heads": Hkv,
                    "head_dim": D, "context": int(np.max(seq_lens)),
                    "total_tokens": int(np.sum(seq_lens)), "block_size": bs,
-                   "split_tokens": split, "cache_copies_rotated": args.copies,
+                   "split_tokens": split, "split_tokens_planned": split_plan,
+                   "split_sweep_us_per_step": {str(k): round(v * 1e3, 2)
+                                               for k, v in split_tried.items()},
+                   "cache_copies_rotated": args.copies,
                    "decode_kernel": kind, "parallelism": "single GPU"},
         "algorithmic_bytes_per_step": alg,
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS,
