@@ -371,7 +371,10 @@ def main(argv=None):
             run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, sp, ws, out, 5, fused=fused)
             split_tried[sp] = run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, sp, ws, out,
                                                max(args.steps // 4, 10), fused=fused)
-        split = min(split_tried, key=split_tried.get)
+        # another split replaces the plan only when clearly faster (3 %), so
+        # that timing noise between close candidates does not pick the worse
+        best = min(split_tried, key=split_tried.get)
+        split = best if split_tried[best] < 0.97 * split_tried[split_plan] else split_plan
         print(f"# split sweep (us/step): " +
               ", ".join(f"{k}: {v * 1e3:.1f}" for k, v in split_tried.items()) +
               f" -> {split}", file=sys.stderr, flush=True)
