@@ -116,6 +116,8 @@ CASES = [
     ("kint8_row_vint4_g4", [777, 64], 32, 8, 128, 2, 1, 128, 32),
     ("kint8_row_vsym_g5", [1030], 40, 8, 128, 2, 0, 128, 32),
     ("kint8_row_hkv4_valu", [400], 20, 4, 128, 2, 1, 128, 32),
+    ("kint8_row_g5_short", [1, 2, 17, 31, 32, 33], 40, 8, 128, 2, 1, 128, 32),
+    ("int4_g6_two_sets_short", [1, 16, 47], 48, 8, 128, 0, 0, 32, 32),
 ]
 
 
@@ -257,3 +259,23 @@ def test_kernel_kind_dispatch():
     assert kk(32, 8, 128, _lib.KV_INT8_SYM, 64, _lib.KV_INT4_ASYM, 32) == "valu"
     assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT4_ASYM, 32) == "valu"
     assert kk(32, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT8_SYM, 32) == "valu"
+
+
+@pytest.mark.parametrize("kfmt,vfmt,hkv,hq", [(0, 1, 8, 32), (1, 0, 8, 40), (0, 1, 4, 16),
+                                              (1, 0, 4, 16)],
+                         ids=["ksym_vasym_coop", "kasym_vsym_coop_two_sets", "ksym_vasym_perhead",
+                              "kasym_vsym_perhead"])
+def test_mixed_int4_formats_through_the_abi(kfmt, vfmt, hkv, hq):
+    """K and V planes with different INT4 encodings (the reference's Python
+    API ties them to one flag; the C ABI takes one format per plane)."""
+    from knlp_amd import ops
+    seq_lens = [700, 33, 1]
+    bt, kp, vp = _build(seq_lens, hq, hkv, 128, kfmt, vfmt, 32, 32, 77)
+    q = _query(len(seq_lens), hq, 128, 77)
+    kd, ks, kz = kvgen.plane_to_torch(kp, DEV)
+    vd, vs, vz = kvgen.plane_to_torch(vp, DEV)
+    out = ops._decode(q.to(DEV), ops._plane(kd, ks, kz, kfmt, 32), ops._plane(vd, vs, vz, vfmt, 32),
+                      16, torch.from_numpy(bt).to(DEV),
+                      torch.tensor(seq_lens, dtype=torch.int32, device=DEV), hkv, 128)
+    torch.cuda.synchronize()
+    _check(out, q, kp, vp, bt, seq_lens)
