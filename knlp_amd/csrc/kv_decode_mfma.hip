@@ -298,8 +298,8 @@ struct WaveState {
   float m_run[GPL];    // running max per q head (score units of 2^-24)
   float lsum[GPL];     // per-lane partial softmax sums
   float zacc[4];       // per-lane zero-point term, rows 4blk + e
-  float sl2;           // softmax_scale * log2(e) * 2^24
-  float thr;           // rescale threshold 2 / sl2 (score units)
+  float sl2[GPL];      // softmax_scale * log2(e) * 2^24 / (the row's q scale)
+  float thr[GPL];      // rescale threshold 2 / sl2 (score units)
 
   // Scores of the two sub-tiles in units of 2^-24:
   //   sum_kg s[t,kg] * S[(g,kg),t] + z[t,kg] * qsum24[(g,kg)].
@@ -335,7 +335,7 @@ struct WaveState {
   __device__ __forceinline__ bool max_moves(const float (&score)[2][GPL]) const {
     bool up = false;
 #pragma unroll
-    for (int gi = 0; gi < GPL; ++gi) up |= fmaxf(score[0][gi], score[1][gi]) > m_run[gi] + thr;
+    for (int gi = 0; gi < GPL; ++gi) up |= fmaxf(score[0][gi], score[1][gi]) > m_run[gi] + thr[gi];
     return __any(up);
   }
 
@@ -346,8 +346,8 @@ struct WaveState {
 #pragma unroll
     for (int gi = 0; gi < GPL; ++gi) {
       const float tmax = row_max16(fmaxf(score[0][gi], score[1][gi]));
-      const bool up = tmax > m_run[gi] + thr;
-      alpha[gi] = up ? __builtin_amdgcn_exp2f((m_run[gi] - tmax) * sl2) : 1.0f;
+      const bool up = tmax > m_run[gi] + thr[gi];
+      alpha[gi] = up ? __builtin_amdgcn_exp2f((m_run[gi] - tmax) * sl2[gi]) : 1.0f;
       m_run[gi] = up ? tmax : m_run[gi];
     }
 #pragma unroll
@@ -374,7 +374,7 @@ struct WaveState {
 #pragma unroll
       for (int gi = 0; gi < GPL; ++gi) {
         // (score - max) first: the token that sets the max gets p = 1 exactly
-        p[gi] = __builtin_amdgcn_exp2f((score[x][gi] - m_run[gi]) * sl2);   // 0 when masked
+        p[gi] = __builtin_amdgcn_exp2f((score[x][gi] - m_run[gi]) * sl2[gi]);   // 0 when masked
         lsum[gi] += p[gi];
       }
       float sv[4], P[4];
@@ -546,7 +546,12 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   const int gs = K8 ? D / NG : a.kp.group_size;
   const int rows = nh * NG;
   // ---- masked q (row r = col): this lane's D/4 consecutive elements ----------
+  // A bf16 q enters the fp16 A operand scaled by a power of two per head,
+  // qscale = 2^(14 - e) with max|q_head| < 2^e: exact for every element down
+  // to 2^-28 of the head's maximum (fp16 holds bf16's 8-bit mantissa), and
+  // the scale leaves the scores through the row's softmax scale.
   float qpart = 0.0f;
+  float qscale = 1.0f;
   {
     const int r = col;
     const int g = r < rows ? r / NG : 0;
@@ -564,12 +569,25 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
         qv[8 * i + 2 * j + 1] = static_cast<uint16_t>(ws[j] >> 16);
       }
     }
+    if (a.q_bf16) {
+      float mx = 0.0f;
+#pragma unroll
+      for (int i = 0; i < D / 4; ++i) mx = fmaxf(mx, fabsf(bf16_bits_to_float(qv[i])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));   // the four lane blocks hold the head
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      int ex = 0;
+      frexpf(mx, &ex);
+      qscale = mx > 0.0f ? ldexpf(1.0f, 14 - ex) : 1.0f;
+    }
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int el = 8 * c + (K8 ? kByteK8[e] : kNibK[e]);
-        const _Float16 v = on ? __builtin_bit_cast(_Float16, qv[el]) : _Float16(0);
+        const _Float16 v =
+            !on ? _Float16(0)
+                : a.q_bf16 ? static_cast<_Float16>(bf16_bits_to_float(qv[el]) * qscale)
+                           : __builtin_bit_cast(_Float16, qv[el]);
         // odd nibbles arrive as 16 n: their q slot holds q / 16 (exact
         // unless |q| < 2^-10, where the fp16 subnormal keeps an absolute
         // error below 2^-25); INT8 codes arrive as n + 128
@@ -601,8 +619,13 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.zacc[e] = 0.0f;
-  W.sl2 = a.scale_log2 * 0x1p24f;      // scores are in units of 2^-24
-  W.thr = kRescaleLog2 / W.sl2;
+  // scores are in units of 2^-24 times the row's q scale
+#pragma unroll
+  for (int gi = 0; gi < GPL; ++gi) {
+    const float qs = __shfl(qscale, 4 * blk + gi * NG, kWave);
+    W.sl2[gi] = a.scale_log2 * 0x1p24f / qs;
+    W.thr[gi] = kRescaleLog2 / W.sl2[gi];
+  }
 }
 
 // Reduce over tokens and write the wave's partial (acc, max, sum).  COLS:
@@ -645,7 +668,7 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
       const int g = (4 * blk) / NG + gi;
       if (g < G) {
         const int64_t row = (row0 + g) * a.num_splits + split;
-        a.part_ml[2 * row] = W.m_run[gi] * W.sl2;
+        a.part_ml[2 * row] = W.m_run[gi] * W.sl2[gi];
         a.part_ml[2 * row + 1] = W.lsum[gi];
       }
     }
@@ -1151,14 +1174,15 @@ int heads_per_block_mfma(int num_kv_heads) {
 }  // namespace
 
 // Shapes the matrix-core path takes: INT4 V with 1, 2 or 4 scale groups,
-// fp16 q, D = 64 or 128, K packed INT4 with V's groups or (D = 128) INT8 with
+// fp16 or bf16 q, D = 64 or 128, K packed INT4 with V's groups or (D = 128) INT8 with
 // one scale per row or V's groups, and at most two head sets of 16 rows.  The
 // per-head kernel covers INT4 K with one head set; the other shapes need the
 // cooperative kernel's dense layout and otherwise run on the VALU kernel.
 bool mfma_supported(int group, int head_size, int k_format, int k_gs, int v_format, int v_gs,
                     int q_bf16) {
   const auto int4 = [](int f) { return f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM; };
-  if (!int4(v_format) || q_bf16 || v_gs <= 0) return false;
+  (void)q_bf16;        // bf16 q is converted exactly in init_wave
+  if (!int4(v_format) || v_gs <= 0) return false;
   if (head_size != 64 && head_size != 128) return false;
   if (head_size % v_gs) return false;
   const int ng = head_size / v_gs;

@@ -142,6 +142,34 @@ def test_bf16_query_output_rounding():
     assert (err <= ATOL + 2.0 ** -7 * np.abs(ref)).all()
 
 
+BF16_CASES = [
+    # name, seq_lens, hq, hkv, d, kfmt, vfmt, kgs, vgs, q magnitude
+    ("coop_asym", [1300, 5, 33], 32, 8, 128, 1, 1, 32, 32, 1.0),
+    ("coop_sym_large_q", [700], 32, 8, 128, 0, 0, 32, 32, 3000.0),
+    ("coop_small_q", [700], 32, 8, 128, 1, 1, 32, 32, 1e-3),
+    ("perhead_hkv4", [900, 17], 16, 4, 128, 1, 1, 32, 32, 1.0),
+    ("d64_g2", [500], 16, 8, 64, 1, 1, 32, 32, 1.0),
+    ("kint8_two_sets", [1100, 3], 40, 8, 128, 2, 1, 128, 32, 1.0),
+]
+
+
+@pytest.mark.parametrize("case", BF16_CASES, ids=[c[0] for c in BF16_CASES])
+def test_bf16_query_on_matrix_cores(case):
+    """bf16 q on the MFMA kernels: exact conversion to fp16 under a per-head
+    power-of-two scale, including q far outside [2^-14, 2^15] before it."""
+    name, seq_lens, hq, hkv, d, kf, vf, kgs, vgs, mag = case
+    assert K.decode_kernel_kind(hq, hkv, d, kf, kgs, vf, vgs, torch.bfloat16) == "mfma"
+    bt, kp, vp = _build(seq_lens, hq, hkv, d, kf, vf, kgs, vgs, 300 + len(name))
+    q = (_query(len(seq_lens), hq, d, 300 + len(name), torch.float32) * mag).to(torch.bfloat16)
+    out = _run(q, kp, vp, bt, seq_lens, hkv, d)
+    assert out.dtype == torch.bfloat16
+    ref = A.decode_reference(q.float().numpy(), kp, vp, bt, seq_lens, round_output=False)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    # fp32 bar plus the bf16 output rounding (relative 2^-8, one ulp 2^-7)
+    assert (np.abs(got - ref) <= ATOL + 2.0 ** -7 * np.abs(ref)).all()
+
+
 def test_edge_lengths_zero_one_and_boundaries():
     seq_lens = [0, 1, 63, 64, 65, 255, 256, 257]
     bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, 31)
@@ -247,7 +275,7 @@ def test_kernel_kind_dispatch():
     assert kk(32, 8, 128, _lib.KV_INT4_SYM, 64, _lib.KV_INT4_SYM, 64) == "mfma"
     assert kk(12, 12, 64, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "mfma"
     assert kk(32, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32,
-              torch.bfloat16) == "valu"
+              torch.bfloat16) == "mfma"
     assert kk(64, 8, 256, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "valu"
     # INT8 K (per-row or V's groups) with INT4 V, and up to two 16-row head
     # sets, take the matrix cores when the caches are densely laid out
