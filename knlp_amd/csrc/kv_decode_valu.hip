@@ -32,27 +32,62 @@ struct RowLoad {
   float s, z;   // group scale and zero-point (z folds the -8 offset of INT4 sym)
 };
 
+// Raw bits of one lane's slice of a row: loaded a step ahead of their use,
+// converted by to_row8 when the step computes.
 template <int S>
-__device__ __forceinline__ void load_row8(const knlp_kv_plane& P, int64_t page, int64_t off,
-                                          int head, int c, int grp, RowLoad<S>& r) {
+struct RawRow;
+template <>
+struct RawRow<kInt4> {
+  uint32_t w;
+  uint16_t s, z;
+};
+template <>
+struct RawRow<kInt8> {
+  uint2 w;
+  uint16_t s, z;
+};
+template <>
+struct RawRow<kFp16> {
+  uint4 w;
+};
+
+template <int S>
+__device__ __forceinline__ void load_raw(const knlp_kv_plane& P, int64_t page, int64_t off,
+                                         int head, int c, int grp, RawRow<S>& r) {
   const int64_t base = page * P.stride_block + off * P.stride_page + head * P.stride_head;
   if constexpr (S == kInt4) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(
-        static_cast<const uint8_t*>(P.data) + base + 4 * c);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r.x[e] = static_cast<float>((w >> (4 * e)) & 0xFu);
+    r.w = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(P.data) + base + 4 * c);
   } else if constexpr (S == kInt8) {
-    const uint2 w = *reinterpret_cast<const uint2*>(
-        static_cast<const int8_t*>(P.data) + base + 8 * c);
+    r.w = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(P.data) + base + 8 * c);
+  } else {
+    r.w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(P.data) + base + 8 * c);
+  }
+  if constexpr (S != kFp16) {
+    r.s = (static_cast<const uint16_t*>(P.scales) + page * P.s_stride_block +
+           off * P.s_stride_page + head * P.s_stride_head)[grp];
+    r.z = P.format == KNLP_KV_INT4_ASYM
+              ? (static_cast<const uint16_t*>(P.zeros) + page * P.z_stride_block +
+                 off * P.z_stride_page + head * P.z_stride_head)[grp]
+              : static_cast<uint16_t>(0);
+  }
+}
+
+// Raw bits -> the lane's 8 elements as exact floats, and the group's scale and
+// zero-point (the symmetric INT4 zero is the -8 offset times the scale).
+template <int S>
+__device__ __forceinline__ void to_row8(const knlp_kv_plane& P, const RawRow<S>& w,
+                                        RowLoad<S>& r) {
+  if constexpr (S == kInt4) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.x[e] = static_cast<float>((w.w >> (4 * e)) & 0xFu);
+  } else if constexpr (S == kInt8) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      r.x[e] = static_cast<float>(static_cast<int8_t>((w.x >> (8 * e)) & 0xFFu));
-      r.x[4 + e] = static_cast<float>(static_cast<int8_t>((w.y >> (8 * e)) & 0xFFu));
+      r.x[e] = static_cast<float>(static_cast<int8_t>((w.w.x >> (8 * e)) & 0xFFu));
+      r.x[4 + e] = static_cast<float>(static_cast<int8_t>((w.w.y >> (8 * e)) & 0xFFu));
     }
   } else {
-    const uint4 w = *reinterpret_cast<const uint4*>(
-        static_cast<const uint16_t*>(P.data) + base + 8 * c);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t ws[4] = {w.w.x, w.w.y, w.w.z, w.w.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       r.x[2 * e] = half_bits_to_float(static_cast<uint16_t>(ws[e] & 0xFFFFu));
@@ -60,18 +95,9 @@ __device__ __forceinline__ void load_row8(const knlp_kv_plane& P, int64_t page, 
     }
   }
   if constexpr (S != kFp16) {
-    const uint16_t* sc = static_cast<const uint16_t*>(P.scales) + page * P.s_stride_block +
-                         off * P.s_stride_page + head * P.s_stride_head;
-    r.s = half_bits_to_float(sc[grp]);
-    if (P.format == KNLP_KV_INT4_ASYM) {
-      const uint16_t* zp = static_cast<const uint16_t*>(P.zeros) + page * P.z_stride_block +
-                           off * P.z_stride_page + head * P.z_stride_head;
-      r.z = half_bits_to_float(zp[grp]);
-    } else if (P.format == KNLP_KV_INT4_SYM) {
-      r.z = -8.0f * r.s;            // (n - 8) * s = n * s - 8 s
-    } else {
-      r.z = 0.0f;
-    }
+    r.s = half_bits_to_float(w.s);
+    r.z = P.format == KNLP_KV_INT4_ASYM ? half_bits_to_float(w.z)
+        : P.format == KNLP_KV_INT4_SYM ? -8.0f * r.s : 0.0f;
   } else {
     r.s = 1.0f;
     r.z = 0.0f;
@@ -131,15 +157,43 @@ __global__ __launch_bounds__(512) void decode_valu_kernel(DecodeArgs a) {
   const int32_t* bt = a.block_table + seq * a.bt_stride;
   const int bs = a.block_size;
 
-  for (int t0 = t_begin; t0 < t_end; t0 += TOK) {
+  // Software pipeline over token steps: the block-table entry of step i + 2
+  // and the K / V rows of step i + 1 are loaded while step i computes.  The
+  // pure fp16 pair keeps the unpipelined order, which measured faster for it
+  // (its rows are 4x larger: the second register set costs occupancy).
+  constexpr bool PIPE = !(KS == kFp16 && VS == kFp16);
+  auto token_of = [&](int t0) {
     const int t = t0 + tk;
-    const bool valid = t < t_end;
-    const int tt = valid ? t : t_begin;
+    return t < t_end ? t : t_begin;
+  };
+  int32_t page1 = 0, page2 = 0;                      // pages of steps i + 1, i + 2
+  RawRow<KS> kraw, kraw1;
+  RawRow<VS> vraw, vraw1;
+  {
+    const int tt = token_of(t_begin);
     const int64_t page = bt[tt / bs];
-    const int64_t off = tt % bs;
+    load_raw<KS>(a.kp, page, tt % bs, kvh, c, kgrp, kraw);
+    load_raw<VS>(a.vp, page, tt % bs, kvh, c, vgrp, vraw);
+    if (PIPE && t_begin + TOK < t_end) page1 = bt[token_of(t_begin + TOK) / bs];
+  }
+  for (int t0 = t_begin; t0 < t_end; t0 += TOK) {
+    const bool valid = t0 + tk < t_end;
+    if constexpr (PIPE) {
+      if (t0 + 2 * TOK < t_end) page2 = bt[token_of(t0 + 2 * TOK) / bs];
+      if (t0 + TOK < t_end) {
+        const int tt = token_of(t0 + TOK);
+        load_raw<KS>(a.kp, page1, tt % bs, kvh, c, kgrp, kraw1);
+        load_raw<VS>(a.vp, page1, tt % bs, kvh, c, vgrp, vraw1);
+      }
+    } else if (t0 != t_begin) {
+      const int tt = token_of(t0);
+      const int64_t page = bt[tt / bs];
+      load_raw<KS>(a.kp, page, tt % bs, kvh, c, kgrp, kraw);
+      load_raw<VS>(a.vp, page, tt % bs, kvh, c, vgrp, vraw);
+    }
 
     RowLoad<KS> kr;
-    load_row8<KS>(a.kp, page, off, kvh, c, kgrp, kr);
+    to_row8<KS>(a.kp, kraw, kr);
     float part[GB];
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
@@ -180,7 +234,7 @@ __global__ __launch_bounds__(512) void decode_valu_kernel(DecodeArgs a) {
       }
     }
     RowLoad<VS> vr;
-    load_row8<VS>(a.vp, page, off, kvh, c, vgrp, vr);
+    to_row8<VS>(a.vp, vraw, vr);
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
       const float p = exp2f(part[g] - m[g]);         // invalid token: exp2(-inf) = 0
@@ -189,6 +243,11 @@ __global__ __launch_bounds__(512) void decode_valu_kernel(DecodeArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv, vr.x[e], acc[g][e]);
       zacc[g] = fmaf(p, vr.z, zacc[g]);
+    }
+    if constexpr (PIPE) {
+      kraw = kraw1;
+      vraw = vraw1;
+      page1 = page2;
     }
   }
 
