@@ -157,16 +157,17 @@ int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads, int3
     return KNLP_ERR_SHAPE;
   (void)num_q_heads;
   // Aim for about two resident workgroups per CU over the whole batch (one
-  // for the cooperative matrix-core kernel -- INT4 V, INT4 or (D = 128) INT8
-  // K, Hkv % 8 == 0 -- which runs one 8-wave block per CU holding 100-160 KB
+  // for the cooperative matrix-core kernel -- INT4 or INT8 codes (INT8 at
+  // D = 128), Hkv % 8 == 0 -- which runs one 8-wave block per CU holding 100-160 KB
   // of LDS tile buffers, so that every block starts in the first round), in
   // multiples of 64 tokens.  Small batches get short splits down to 64
   // tokens (config 1, one 1024-token sequence: 9.6 us per step at 64 tokens
   // against 17 us at 256); partials cost (D+2)*4 bytes per q head and split
   // on each side of the merge, negligible at that size.
   const auto int4 = [](int f) { return f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM; };
-  const bool wide = num_kv_heads % 8 == 0 && int4(v_format) &&
-                    (int4(k_format) || (k_format == KNLP_KV_INT8_SYM && head_size == 128));
+  const auto int8_128 = [&](int f) { return f == KNLP_KV_INT8_SYM && head_size == 128; };
+  const bool wide = num_kv_heads % 8 == 0 && (int4(v_format) || int8_128(v_format)) &&
+                    (int4(k_format) || int8_128(k_format));
   const int hpb = wide ? 8 : heads_per_block(num_kv_heads);
   const int64_t groups =
       static_cast<int64_t>(num_seqs) * ((num_kv_heads + hpb - 1) / hpb);

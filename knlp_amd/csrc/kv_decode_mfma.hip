@@ -50,6 +50,8 @@
 // exceeds it by more than 2 (log2 units).  Then p <= 4 and |P'| <= 4 * s_v,
 // which stays inside fp16 range for any finite fp16 K/V input (s_v < 9400).
 
+#include <type_traits>
+
 #include "kv_decode.h"
 
 namespace knlp {
@@ -279,9 +281,12 @@ __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane,
 // the general path: masked scores, raise_max, masked accumulate.  Both paths
 // do the same arithmetic on rows whose max does not move, so the result does
 // not depend on which path a tile took.
-template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH, int NGK = NG>
+template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH, int NGK = NG, bool V8 = false>
 struct WaveState {
   static constexpr int GPL = 4 / NG;
+  // V codes: packed INT4 (one dword of 8 nibble-columns per token and lane in
+  // pv_columns) or INT8 (V8: 8 bytes)
+  using VWord = typename std::conditional<V8, uint2, uint32_t>::type;
   // INT8 K codes: two dwords per QK chunk, one scale per NG / NGK row groups
   static constexpr bool K8 = KCH == 2 * NCH;
   using ST = SubTile<NCH, NG, KCH, NGK>;
@@ -388,7 +393,8 @@ struct WaveState {
           if constexpr (MASK) zv = valid[x] ? zv : 0.0f;
           zacc[e] = fmaf(p[e / NG], zv, zacc[e]);
         } else {
-          zacc[e] = fmaf(-8.0f, P[e], zacc[e]);          // symmetric: zero = -8 s
+          // symmetric: zero = -8 s (INT4) or -128 s (INT8 codes biased by 128)
+          zacc[e] = fmaf(V8 ? -128.0f : -8.0f, P[e], zacc[e]);
         }
       }
       const h2 hi01 = {static_cast<_Float16>(P[0]), static_cast<_Float16>(P[1])};
@@ -476,6 +482,41 @@ struct WaveState {
     }
   }
 
+  // PV with INT8 V codes read from LDS as lane = column: vw[x][i] holds the
+  // 8 bytes of columns 8 col .. 8 col + 7 of token 16x + 4blk + i.  The codes
+  // are biased by 128 (xor 0x80), then column j takes byte j of a token pair
+  // into the two halves of a dword with one v_perm: the fp16 subnormals
+  // (n + 128) 2^-24 of slots (2q, 2q + 1); the bias returns through zacc.
+  // Accumulator j = 2c + h holds column 8 col + j.
+  __device__ __forceinline__ void pv_columns(const uint2 (&vw)[2][4], const h8& ahi,
+                                             const h8& alo) {
+    uint32_t w[2][2][4];      // [column half][x][i], biased
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w[0][x][i] = vw[x][i].x ^ 0x80808080u;
+        w[1][x][i] = vw[x][i].y ^ 0x80808080u;
+      }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * c + h;
+        const uint32_t sel = static_cast<uint32_t>(j % 4) | (0x0Cu << 8) |
+                             (static_cast<uint32_t>(4 + j % 4) << 16) | (0x0Cu << 24);
+        u4 bw;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bw[q] = __builtin_amdgcn_perm(w[j / 4][q / 2][2 * (q % 2) + 1],
+                                        w[j / 4][q / 2][2 * (q % 2)], sel);
+        const h8 bv = __builtin_bit_cast(h8, bw);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
+      }
+    }
+  }
+
   template <bool MASK>
   __device__ __forceinline__ void accumulate(const ST (&st)[2],
                                              const bool (&valid)[2],
@@ -483,16 +524,6 @@ struct WaveState {
     h8 ahi, alo;
     probs<MASK>(st, valid, score, ahi, alo);
     pv_transposed(st, ahi, alo);
-  }
-
-  template <bool MASK>
-  __device__ __forceinline__ void accumulate_cols(const ST (&st)[2],
-                                                  const uint32_t (&vw)[2][4],
-                                                  const bool (&valid)[2],
-                                                  const float (&score)[2][GPL]) {
-    h8 ahi, alo;
-    probs<MASK>(st, valid, score, ahi, alo);
-    pv_columns(vw, ahi, alo);
   }
 
   // General step: any tile, masked or not, max moving or not.
@@ -510,20 +541,6 @@ struct WaveState {
     accumulate<MASK>(st, valid, score);
   }
 
-  template <bool MASK>
-  __device__ __forceinline__ void step_cols(const ST (&st)[2],
-                                            const uint32_t (&vw)[2][4], int tbase, int t_end,
-                                            int col) {
-    bool valid[2] = {true, true};
-    if constexpr (MASK) {
-      valid[0] = tbase + col < t_end;
-      valid[1] = tbase + 16 + col < t_end;
-    }
-    float score[2][GPL];
-    scores<MASK>(st, valid, score);
-    if (max_moves(score)) raise_max(score);
-    accumulate_cols<MASK>(st, vw, valid, score);
-  }
 };
 
 // Query heads per head set: a set fills the 16 rows of one 16x16 MFMA.
@@ -532,8 +549,8 @@ __host__ __device__ constexpr int heads_per_set() { return 16 / NG; }
 
 // q, constants and accumulators of the wave serving kv head `kvh`, for the
 // head set whose first query head (within the kv head's group) is `hs`.
-template <int D, int NG, bool KASYM, bool VASYM, int KCH = D / 32, int NGK = NG>
-__device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK>& W,
+template <int D, int NG, bool KASYM, bool VASYM, int KCH = D / 32, int NGK = NG, bool V8 = false>
+__device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8>& W,
                                           const DecodeArgs& a, int seq, int kvh, int col,
                                           int blk, int hs = 0) {
   constexpr int NCH = D / 32;
@@ -631,8 +648,8 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
 // Reduce over tokens and write the wave's partial (acc, max, sum).  COLS:
 // the accumulators follow pv_columns' column order, else pv_transposed's.
 template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false, int KCH = D / 32,
-          int NGK = NG>
-__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK>& W,
+          int NGK = NG, bool V8 = false>
+__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8>& W,
                                                const DecodeArgs& a, int seq, int kvh,
                                                int split, int col, int blk, int hs = 0) {
   constexpr int NCH = D / 32;
@@ -656,8 +673,9 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
         const int g = r / NG;
         if (g < G && d / gs == r % NG) {
           const int64_t row = (row0 + g) * a.num_splits + split;
-          // pv_columns' odd columns carry a factor 16
-          a.part_o[row * D + d] = fmaf(W.acc[c][h][i], COLS && h ? 0x1p20f : 0x1p24f, W.zacc[i]);
+          // pv_columns' odd INT4 columns carry a factor 16
+          a.part_o[row * D + d] =
+              fmaf(W.acc[c][h][i], COLS && h && !V8 ? 0x1p20f : 0x1p24f, W.zacc[i]);
         }
       }
     }
@@ -785,11 +803,11 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
 // staged tile and, after common-subexpression elimination, its K and V
 // conversions.
 // ---------------------------------------------------------------------------
-template <int D, int NG, bool K8 = false, int NGK = NG>
+template <int D, int NG, bool K8 = false, int NGK = NG, bool V8 = false>
 struct CoopLayout {
   static constexpr int kHeads = 8;
   static constexpr int HBK = K8 ? D : D / 2;       // K code bytes per head and token
-  static constexpr int HBV = D / 2;                // V code bytes per head and token
+  static constexpr int HBV = V8 ? D : D / 2;       // V code bytes per head and token
   static constexpr int SBK = 2 * NGK;              // K scale bytes per head and token
   static constexpr int SBV = 2 * NG;               // V scale bytes per head and token
   static constexpr int CROWK = kHeads * HBK;       // LDS rows (16 rows per sub-tile)
@@ -812,7 +830,7 @@ struct CoopLayout {
   // LDS tile buffers at one block per CU (160 KB): copies run NBUF - 1 tiles ahead
   static constexpr int NBUF = 4 * BYTES <= 160 * 1024 ? 4 : 3 * BYTES <= 160 * 1024 ? 3 : 2;
   static_assert(NBUF * BYTES <= 160 * 1024, "tile buffers fit one CU's LDS");
-  static_assert(CPSK % 4 == 0 && CPSV % 4 == 0 && NPWK >= 1 && NPWK <= 4 && NPWV <= 2,
+  static_assert(CPSK % 4 == 0 && CPSV % 4 == 0 && NPWK >= 1 && NPWK <= 4 && NPWV <= 4,
                 "each sub-tile's code parts split evenly over its 4 waves");
   static_assert(16 * SROWK <= 1024 && 16 * SROWV <= 1024, "one wave copy per scale sub-tile");
   // scale array a: 0 K scales, 1 V scales, 2 K zeros, 3 V zeros
@@ -846,7 +864,7 @@ struct CoopAddr {
   const uint8_t* vc;
   const uint8_t* sp;      // this wave's scale array, head h0
   uint32_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
-  uint32_t lk[4], lv[2], ls;   // lane byte offsets in HBM (code parts, scale chunk)
+  uint32_t lk[4], lv[4], ls;   // lane byte offsets in HBM (code parts, scale chunk)
   bool same_kv;           // K and V codes share their strides (one page offset)
   bool s_arr_on;          // this wave copies a scale array (wave-uniform)
   bool s_on;              // this lane copies a scale chunk
@@ -973,16 +991,19 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
 // D/32 bytes at columns (D/16)*col.. of token 16x + 4blk + i.  The four lane
 // blocks read rows 4blk + i, whose chunk swizzles differ, so the 64 lanes
 // hit 64 distinct banks.
-template <class L, int D>
+template <class L, int D, class VW>
 __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int col, int blk,
-                                            uint32_t (&vw)[2][4]) {
+                                            VW (&vw)[2][4]) {
+  constexpr int CB = L::HBV / 16;      // V code bytes per lane and token: 8 columns
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int o = L::V_OFF + x * 16 * L::CROWV +
-                    L::code_off(L::CROWV, 4 * blk + i, wave * L::HBV + (D / 32) * col);
-      if constexpr (D == 128)
+                    L::code_off(L::CROWV, 4 * blk + i, wave * L::HBV + CB * col);
+      if constexpr (CB == 8)
+        vw[x][i] = *reinterpret_cast<const uint2*>(buf + o);
+      else if constexpr (CB == 4)
         vw[x][i] = *reinterpret_cast<const uint32_t*>(buf + o);
       else
         vw[x][i] = *reinterpret_cast<const uint16_t*>(buf + o);
@@ -1001,7 +1022,8 @@ __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int co
 template <class L, int D, int NSET, bool MASK, bool PV_PREV, class WS>
 __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int i, int ntiles,
                                           int t_begin, int t_end, int wave, int col, int blk,
-                                          const uint8_t* cur, uint8_t* nxt, uint32_t (&vw)[2][4],
+                                          const uint8_t* cur, uint8_t* nxt,
+                                          typename WS::VWord (&vw)[2][4],
                                           h8 (&ahi)[NSET], h8 (&alo)[NSET], PageWindow& PW,
                                           int lane) {
   constexpr int NBUF = L::NBUF;
@@ -1037,15 +1059,15 @@ __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int 
 // One block per CU (8 waves), L::NBUF tile buffers of LDS: the copies run
 // NBUF - 1 tiles ahead of the compute.  K8: INT8 K codes with NGK scale
 // groups; NSET head sets per wave.
-template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET>
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_mfma_coop_kernel(DecodeArgs a) {
-  using L = CoopLayout<D, NG, K8, NGK>;
+  using L = CoopLayout<D, NG, K8, NGK, V8>;
   constexpr int NCH = D / 32;
   constexpr int KCH = K8 ? 2 * NCH : NCH;
   constexpr int NBUF = L::NBUF;
-  using WS = WaveState<NCH, NG, KASYM, VASYM, KCH, NGK>;
-  static_assert(!(K8 && KASYM), "INT8 K is symmetric");
+  using WS = WaveState<NCH, NG, KASYM, VASYM, KCH, NGK, V8>;
+  static_assert(!(K8 && KASYM) && !(V8 && VASYM), "INT8 codes are symmetric");
   __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][L::BYTES];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -1069,8 +1091,8 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   WS W[NSET];
 #pragma unroll
   for (int s = 0; s < NSET; ++s)
-    init_wave<D, NG, KASYM, VASYM, KCH, NGK>(W[s], a, seq, kvh, col, blk,
-                                             s * heads_per_set<NG>());
+    init_wave<D, NG, KASYM, VASYM, KCH, NGK, V8>(W[s], a, seq, kvh, col, blk,
+                                                 s * heads_per_set<NG>());
 
   CoopAddr C;
   {
@@ -1093,7 +1115,7 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
       C.lk[k] = static_cast<uint32_t>(r * K.stride_page + 16 * c);
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < 4; ++k) {
       const int byte = ((wave >> 1) + 4 * k) % L::CPSV * 1024 + 16 * lane;
       const int r = byte / L::CROWV;
       const int c = ((byte % L::CROWV) >> 4) ^ r;
@@ -1141,7 +1163,7 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
   // the PV of the last tile
-  uint32_t vw[2][4];
+  typename WS::VWord vw[2][4];
   h8 ahi[NSET], alo[NSET];
   const int nfull = (t_end - t_begin) / 32;
 #define KNLP_COOP_TILE(MASK, PV_PREV)                                                       \
@@ -1160,8 +1182,8 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
 #pragma unroll
   for (int s = 0; s < NSET; ++s) {
     W[s].pv_columns(vw, ahi[s], alo[s]);
-    write_partials<D, NG, KASYM, VASYM, true, KCH, NGK>(W[s], a, seq, kvh, split, col, blk,
-                                                        s * heads_per_set<NG>());
+    write_partials<D, NG, KASYM, VASYM, true, KCH, NGK, V8>(W[s], a, seq, kvh, split, col, blk,
+                                                            s * heads_per_set<NG>());
   }
 }
 
@@ -1173,7 +1195,8 @@ int heads_per_block_mfma(int num_kv_heads) {
 
 }  // namespace
 
-// Shapes the matrix-core path takes: INT4 V with 1, 2 or 4 scale groups,
+// Shapes the matrix-core path takes: INT4 V with 1, 2 or 4 scale groups
+// (or, at D = 128, INT8 V with 1 or 4),
 // fp16 or bf16 q, D = 64 or 128, K packed INT4 with V's groups or (D = 128) INT8 with
 // one scale per row or V's groups, and at most two head sets of 16 rows.  The
 // per-head kernel covers INT4 K with one head set; the other shapes need the
@@ -1182,11 +1205,14 @@ bool mfma_supported(int group, int head_size, int k_format, int k_gs, int v_form
                     int q_bf16) {
   const auto int4 = [](int f) { return f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM; };
   (void)q_bf16;        // bf16 q is converted exactly in init_wave
-  if (!int4(v_format) || v_gs <= 0) return false;
+  const bool v8 = v_format == KNLP_KV_INT8_SYM;
+  if (!(int4(v_format) || v8) || v_gs <= 0) return false;
   if (head_size != 64 && head_size != 128) return false;
   if (head_size % v_gs) return false;
   const int ng = head_size / v_gs;
   if (ng != 1 && ng != 2 && ng != 4) return false;
+  // INT8 V: D = 128 with one scale per row or g32 (cooperative kernel only)
+  if (v8 && (head_size != 128 || (ng != 1 && ng != 4))) return false;
   if (int4(k_format)) {
     if (k_gs != v_gs) return false;
   } else if (k_format == KNLP_KV_INT8_SYM) {
@@ -1224,10 +1250,11 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const int ngk = head_size / a.kp.group_size;
   const bool ka = a.kp.format == KNLP_KV_INT4_ASYM;
   const bool va = a.vp.format == KNLP_KV_INT4_ASYM;
+  const bool v8 = a.vp.format == KNLP_KV_INT8_SYM;
   const int nset = (a.group * ng + 15) / 16;
   const bool coop = coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
                     coop_layout_ok(a.vp, head_size, a.num_kv_heads);
-  if (!coop && (k8 || nset > 1))     // only the cooperative kernel has these
+  if (!coop && (k8 || v8 || nset > 1))     // only the cooperative kernel has these
     return launch_decode_valu(a, head_size, heads_per_block_mfma(a.num_kv_heads), stream);
   const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
   const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
@@ -1240,7 +1267,7 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   else if (va) KNLP_LAUNCH(KERNEL<D, NG, false, true __VA_ARGS__>);                       \
   else KNLP_LAUNCH(KERNEL<D, NG, false, false __VA_ARGS__>);
 #define KNLP_INT4(D, NG)                                                                  \
-  if (!k8 && head_size == D && ng == NG) {                                                \
+  if (!k8 && !v8 && head_size == D && ng == NG) {                                         \
     if (coop && nset == 1) {                                                              \
       KNLP_ASYM(decode_mfma_coop_kernel, D, NG, , false, NG, 1)                           \
     } else if (coop) {                                                                    \
@@ -1259,7 +1286,7 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
     else KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, false, true, NGK, 2>);       \
   }
 #define KNLP_INT8K(NG)                                                                    \
-  if (k8 && head_size == 128 && ng == NG) {                                               \
+  if (k8 && !v8 && head_size == 128 && ng == NG) {                                        \
     if (ngk == 1) {                                                                       \
       KNLP_INT8K_SETS(NG, 1)                                                              \
     } else {                                                                              \
@@ -1276,6 +1303,28 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   KNLP_INT8K(4)
   KNLP_INT8K(2)
   KNLP_INT8K(1)
+  // INT8 V (symmetric, biased codes): K INT4 (V's groups) or INT8 (one scale
+  // per row or V's groups)
+#define KNLP_V8_SETS(KA, K8, NG, NGK)                                                    \
+  if (nset == 1) KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, KA, false, K8, NGK, 1, true>); \
+  else KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, KA, false, K8, NGK, 2, true>);
+#define KNLP_V8(NG)                                                                       \
+  if (v8 && head_size == 128 && ng == NG) {                                               \
+    if (k8 && ngk == 1) {                                                                 \
+      KNLP_V8_SETS(false, true, NG, 1)                                                    \
+    } else if (k8) {                                                                      \
+      KNLP_V8_SETS(false, true, NG, NG)                                                   \
+    } else if (ka) {                                                                      \
+      KNLP_V8_SETS(true, false, NG, NG)                                                   \
+    } else {                                                                              \
+      KNLP_V8_SETS(false, false, NG, NG)                                                  \
+    }                                                                                     \
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                   \
+  }
+  KNLP_V8(4)
+  KNLP_V8(1)
+#undef KNLP_V8
+#undef KNLP_V8_SETS
 #undef KNLP_INT8K
 #undef KNLP_INT8K_SETS
 #undef KNLP_INT4

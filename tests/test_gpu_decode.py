@@ -118,6 +118,10 @@ CASES = [
     ("kint8_row_hkv4_valu", [400], 20, 4, 128, 2, 1, 128, 32),
     ("kint8_row_g5_short", [1, 2, 17, 31, 32, 33], 40, 8, 128, 2, 1, 128, 32),
     ("int4_g6_two_sets_short", [1, 16, 47], 48, 8, 128, 0, 0, 32, 32),
+    # INT8 V on the cooperative kernel (per-row and g32 V scales)
+    ("kint8_row_vint8_g32_two_sets", [1100, 5, 33], 40, 8, 128, 2, 2, 128, 32),
+    ("kint8_vint8_row", [640, 17], 32, 8, 128, 2, 2, 128, 128),
+    ("kint8_vint8_hkv4_valu", [300], 16, 4, 128, 2, 2, 32, 32),
 ]
 
 
@@ -286,13 +290,15 @@ def test_kernel_kind_dispatch():
         kk(72, 8, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32)
     assert kk(32, 8, 128, _lib.KV_INT8_SYM, 64, _lib.KV_INT4_ASYM, 32) == "valu"
     assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT4_ASYM, 32) == "valu"
-    assert kk(32, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT8_SYM, 32) == "valu"
+    assert kk(32, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT8_SYM, 32) == "mfma"
+    assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT8_SYM, 32) == "valu"
+    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT4_ASYM, 32) == "valu"
 
 
 @pytest.mark.parametrize("kfmt,vfmt,hkv,hq", [(0, 1, 8, 32), (1, 0, 8, 40), (0, 1, 4, 16),
-                                              (1, 0, 4, 16)],
+                                              (1, 0, 4, 16), (1, 2, 8, 32), (0, 2, 8, 40)],
                          ids=["ksym_vasym_coop", "kasym_vsym_coop_two_sets", "ksym_vasym_perhead",
-                              "kasym_vsym_perhead"])
+                              "kasym_vsym_perhead", "kint4_vint8_coop", "kint4sym_vint8_two_sets"])
 def test_mixed_int4_formats_through_the_abi(kfmt, vfmt, hkv, hq):
     """K and V planes with different INT4 encodings (the reference's Python
     API ties them to one flag; the C ABI takes one format per plane)."""
