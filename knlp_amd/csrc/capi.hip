@@ -51,6 +51,12 @@ int check_plane(const knlp_kv_plane* P, int head_size, bool decode) {
 // single vector loads and takes one page per 16-token sub-tile.
 bool mfma_layout_ok(const knlp_kv_plane& P, int head_size, int block_size) {
   if (block_size < 16 || !is_pow2(block_size)) return false;
+  const auto strides16 = [](const knlp_kv_plane& Q) {
+    return (2 * Q.stride_block) % 16 == 0 && (2 * Q.stride_page) % 16 == 0 &&
+           (2 * Q.stride_head) % 16 == 0;
+  };
+  // fp16 K: each lane reads a quarter row (D/2 bytes) with 16-byte loads
+  if (P.format == KNLP_KV_FP16) return aligned(P.data, 16) && strides16(P);
   const int64_t lb = head_size / 8;
   const int64_t sb = 2 * (head_size / P.group_size);
   const auto strides_ok = [](int64_t a, int64_t b, int64_t c, int64_t m) {

@@ -180,6 +180,20 @@ struct Halves<1> {
 template <int NCH>
 struct Codes;    // NCH dwords of codes per lane and token
 template <>
+struct Codes<16> {   // 64 bytes: a quarter of an fp16 K row at D = 128
+  uint4 v[4];
+  __device__ uint32_t dw(int c) const {
+    const uint4& u = v[c >> 2];
+    const int i = c & 3;
+    return i == 0 ? u.x : i == 1 ? u.y : i == 2 ? u.z : u.w;
+  }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      v[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * k, 0, 0));
+  }
+};
+template <>
 struct Codes<8> {
   uint4 v, w;
   __device__ uint32_t dw(int c) const {
@@ -260,14 +274,15 @@ struct PageWindow {
   }
 };
 
-template <int NCH, int NG, bool KASYM, bool VASYM>
+template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH>
 __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane, int pbase,
-                                         SubTile<NCH, NG>& st) {
+                                         SubTile<NCH, NG, KCH>& st) {
   const int64_t page = P.page(A.bt, lane, pbase >> A.bs_shift);
   const int64_t off0 = pbase & ((1 << A.bs_shift) - 1);
   st.k.load(rsrc_of(A.kc + (page * A.kc_b + off0 * A.kc_p)), A.lkc);
   st.v.load(rsrc_of(A.vc + (page * A.vc_b + off0 * A.vc_p)), A.lvc);
-  st.ks.load(rsrc_of(A.ks + (page * A.ks_b + off0 * A.ks_p)), A.lks);
+  if constexpr (KCH != 4 * NCH)   // fp16 K has no scales
+    st.ks.load(rsrc_of(A.ks + (page * A.ks_b + off0 * A.ks_p)), A.lks);
   st.vs.load(rsrc_of(A.vs + (page * A.vs_b + off0 * A.vs_p)), A.lvs);
   if constexpr (KASYM) st.kz.load(rsrc_of(A.kz + (page * A.kz_b + off0 * A.kz_p)), A.lkz);
   if constexpr (VASYM) st.vz.load(rsrc_of(A.vz + (page * A.vz_b + off0 * A.vz_p)), A.lvz);
@@ -289,10 +304,13 @@ struct WaveState {
   using VWord = typename std::conditional<V8, uint2, uint32_t>::type;
   // INT8 K codes: two dwords per QK chunk, one scale per NG / NGK row groups
   static constexpr bool K8 = KCH == 2 * NCH;
+  // fp16 K: four dwords of halves per QK chunk, used as they are (no scale)
+  static constexpr bool K16 = KCH == 4 * NCH;
   using ST = SubTile<NCH, NG, KCH, NGK>;
   static constexpr bool KZ_USED = KASYM;
   static constexpr bool VZ_USED = VASYM;
-  static_assert(NG % NGK == 0 && (K8 || NGK == NG), "K scale groups nest in the row groups");
+  static_assert(NG % NGK == 0 && (K8 || K16 || NGK == NG),
+                "K scale groups nest in the row groups");
   h8 aq[NCH];          // masked q, A operands of QK (row = col)
   float qsum24[4];     // 2^-24 * sum of q over the group of rows 4blk..4blk+3
   f4 cinit;            // QK accumulator start: 0 for asymmetric INT4 K, else -bias * qsum24
@@ -318,8 +336,10 @@ struct WaveState {
       for (int c = 0; c < NCH; ++c)
         S = __builtin_amdgcn_mfma_f32_16x16x32_f16(
             aq[c],
-            K8 ? bytes_to_h8_sub(st[x].k.dw(2 * c), st[x].k.dw(2 * c + 1))
-               : nibbles_to_h8_sub(st[x].k.dw(c)),
+            K16  ? __builtin_bit_cast(h8, u4{st[x].k.dw(4 * c), st[x].k.dw(4 * c + 1),
+                                             st[x].k.dw(4 * c + 2), st[x].k.dw(4 * c + 3)})
+            : K8 ? bytes_to_h8_sub(st[x].k.dw(2 * c), st[x].k.dw(2 * c + 1))
+                 : nibbles_to_h8_sub(st[x].k.dw(c)),
             S, 0, 0, 0);
 #pragma unroll
       for (int gi = 0; gi < GPL; ++gi) {
@@ -328,7 +348,10 @@ struct WaveState {
         for (int kg = 0; kg < NG; ++kg) {
           const int i = gi * NG + kg;
           if constexpr (KASYM) sc = fmaf(st[x].kz.get(kg), qsum24[i], sc);
-          sc = fmaf(st[x].ks.get(kg * NGK / NG), S[i], sc);
+          if constexpr (K16)
+            sc += S[i];
+          else
+            sc = fmaf(st[x].ks.get(kg * NGK / NG), S[i], sc);
         }
         score[x][gi] = (MASK && !valid[x]) ? -INFINITY : sc;
       }
@@ -556,11 +579,12 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   constexpr int NCH = D / 32;
   constexpr int GPL = 4 / NG;
   constexpr bool K8 = KCH == 2 * NCH;
+  constexpr bool K16 = KCH == 4 * NCH;
   const int G = a.group;
   const int nh = min(heads_per_set<NG>(), G - hs);
   // rows (g, kg): kg is a K scale group for INT4 K; for INT8 K the NG row
   // groups split the head dim in equal parts that share the K scale(s)
-  const int gs = K8 ? D / NG : a.kp.group_size;
+  const int gs = K8 || K16 ? D / NG : a.kp.group_size;
   const int rows = nh * NG;
   // ---- masked q (row r = col): this lane's D/4 consecutive elements ----------
   // A bf16 q enters the fp16 A operand scaled by a power of two per head,
@@ -600,7 +624,7 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
     for (int c = 0; c < NCH; ++c) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int el = 8 * c + (K8 ? kByteK8[e] : kNibK[e]);
+        const int el = 8 * c + (K16 ? e : K8 ? kByteK8[e] : kNibK[e]);
         const _Float16 v =
             !on ? _Float16(0)
                 : a.q_bf16 ? static_cast<_Float16>(bf16_bits_to_float(qv[el]) * qscale)
@@ -608,7 +632,7 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
         // odd nibbles arrive as 16 n: their q slot holds q / 16 (exact
         // unless |q| < 2^-10, where the fp16 subnormal keeps an absolute
         // error below 2^-25); INT8 codes arrive as n + 128
-        W.aq[c][e] = (!K8 && (e & 2)) ? v * static_cast<_Float16>(0.0625f) : v;
+        W.aq[c][e] = (!K8 && !K16 && (e & 2)) ? v * static_cast<_Float16>(0.0625f) : v;
         qpart += static_cast<float>(v);
       }
     }
@@ -619,7 +643,8 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   for (int i = 0; i < 4; ++i) {
     // 2^-24 is exact in fp32: K codes enter the QK product as n * 2^-24
     W.qsum24[i] = __shfl(qpart, 4 * blk + i, kWave) * 0x1p-24f;
-    if constexpr (K8) W.cinit[i] = -128.0f * W.qsum24[i];
+    if constexpr (K16) W.cinit[i] = 0.0f;
+    else if constexpr (K8) W.cinit[i] = -128.0f * W.qsum24[i];
     else if constexpr (!KASYM) W.cinit[i] = -8.0f * W.qsum24[i];
   }
 #pragma unroll
@@ -640,7 +665,8 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
 #pragma unroll
   for (int gi = 0; gi < GPL; ++gi) {
     const float qs = __shfl(qscale, 4 * blk + gi * NG, kWave);
-    W.sl2[gi] = a.scale_log2 * 0x1p24f / qs;
+    // INT4 / INT8 codes enter as n * 2^-24; fp16 K as itself
+    W.sl2[gi] = a.scale_log2 * (K16 ? 1.0f : 0x1p24f) / qs;
     W.thr[gi] = kRescaleLog2 / W.sl2[gi];
   }
 }
@@ -695,10 +721,12 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
 
 // Per-head loads: each wave fetches its own kv head's rows (any layout that
 // passes the alignment checks).  One wave per (sequence, kv head, split).
-template <int D, int NG, bool KASYM, bool VASYM>
+template <int D, int NG, bool KASYM, bool VASYM, bool K16 = false>
 __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   constexpr int NCH = D / 32;    // K-chunks of 32 along head_dim = dwords per lane
-  constexpr int LB = D / 8;      // bytes of codes per lane per token
+  constexpr int LB = D / 8;      // bytes of INT4 codes per lane per token
+  constexpr int KCH = K16 ? 4 * NCH : NCH;   // fp16 K: D/2 bytes per lane per token
+  constexpr int KEB = K16 ? 2 : 1;           // K element bytes (its strides are in elements)
   const int lane = threadIdx.x & (kWave - 1);
   const int col = lane & 15;
   const int blk = lane >> 4;
@@ -717,26 +745,28 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   // the token being decoded, when the caller fused its append into this launch
   decode_append<D>(a, seq, kvh, split, seq_len, lane);
 
-  WaveState<NCH, NG, KASYM, VASYM> W;
-  init_wave<D, NG, KASYM, VASYM>(W, a, seq, kvh, col, blk);
+  WaveState<NCH, NG, KASYM, VASYM, KCH> W;
+  init_wave<D, NG, KASYM, VASYM, KCH>(W, a, seq, kvh, col, blk);
 
   Addr A;
   {
     const knlp_kv_plane& K = a.kp;
     const knlp_kv_plane& V = a.vp;
-    A.kc = static_cast<const uint8_t*>(K.data) + kvh * K.stride_head;
+    A.kc = static_cast<const uint8_t*>(K.data) + KEB * kvh * K.stride_head;
     A.vc = static_cast<const uint8_t*>(V.data) + kvh * V.stride_head;
     A.ks = static_cast<const uint16_t*>(K.scales) + kvh * K.s_stride_head;
     A.vs = static_cast<const uint16_t*>(V.scales) + kvh * V.s_stride_head;
     A.kz = KASYM ? static_cast<const uint16_t*>(K.zeros) + kvh * K.z_stride_head : nullptr;
     A.vz = VASYM ? static_cast<const uint16_t*>(V.zeros) + kvh * V.z_stride_head : nullptr;
-    A.kc_b = K.stride_block; A.kc_p = K.stride_page;
+    A.kc_b = KEB * K.stride_block; A.kc_p = KEB * K.stride_page;
     A.vc_b = V.stride_block; A.vc_p = V.stride_page;
     A.ks_b = K.s_stride_block; A.ks_p = K.s_stride_page;
     A.vs_b = V.s_stride_block; A.vs_p = V.s_stride_page;
     A.kz_b = K.z_stride_block; A.kz_p = K.z_stride_page;
     A.vz_b = V.z_stride_block; A.vz_p = V.z_stride_page;
-    A.lkc = static_cast<uint32_t>(col * K.stride_page + LB * blk);
+    // a lane holds elements 32 blk .. 32 blk + 31 of its token: D/8 bytes of
+    // INT4 codes or D/2 bytes of fp16
+    A.lkc = static_cast<uint32_t>(KEB * col * K.stride_page + (K16 ? D / 2 : LB) * blk);
     A.lvc = static_cast<uint32_t>(col * V.stride_page + LB * blk);
     A.lks = static_cast<uint32_t>(2 * col * K.s_stride_page);
     A.lvs = static_cast<uint32_t>(2 * col * V.s_stride_page);
@@ -755,13 +785,13 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   // can end in a partial tile; that one runs the masked step.  Tiles are
   // visited in increasing order so the page window only moves forward.
   const int ntiles = (t_end - t_begin + 31) / 32;
-  SubTile<NCH, NG> X[2], Y[2];
-  auto load_tile = [&](int tb, SubTile<NCH, NG>(&buf)[2]) {
-    load_sub<NCH, NG, KASYM, VASYM>(A, PW, lane, tb, buf[0]);
+  SubTile<NCH, NG, KCH> X[2], Y[2];
+  auto load_tile = [&](int tb, SubTile<NCH, NG, KCH>(&buf)[2]) {
+    load_sub<NCH, NG, KASYM, VASYM, KCH>(A, PW, lane, tb, buf[0]);
     // a second half wholly past the end re-reads the first half's page (masked)
-    load_sub<NCH, NG, KASYM, VASYM>(A, PW, lane, tb + 16 < t_end ? tb + 16 : tb, buf[1]);
+    load_sub<NCH, NG, KASYM, VASYM, KCH>(A, PW, lane, tb + 16 < t_end ? tb + 16 : tb, buf[1]);
   };
-  auto run_tile = [&](int tb, const SubTile<NCH, NG>(&buf)[2]) {
+  auto run_tile = [&](int tb, const SubTile<NCH, NG, KCH>(&buf)[2]) {
     if (tb + 32 <= t_end)
       W.template step<false>(buf, tb, t_end, col);
     else
@@ -776,7 +806,7 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
     if (i + 2 < ntiles) load_tile(tb + 64, X);
     run_tile(tb + 32, Y);
   }
-  write_partials<D, NG, KASYM, VASYM>(W, a, seq, kvh, split, col, blk);
+  write_partials<D, NG, KASYM, VASYM, false, KCH>(W, a, seq, kvh, split, col, blk);
 }
 
 // ---------------------------------------------------------------------------
@@ -1196,7 +1226,8 @@ int heads_per_block_mfma(int num_kv_heads) {
 }  // namespace
 
 // Shapes the matrix-core path takes: INT4 V with 1, 2 or 4 scale groups
-// (or, at D = 128, INT8 V with 1 or 4),
+// (or, at D = 128, INT8 V with 1 or 4; or fp16 K with INT4 V and one head
+// set, on the per-head kernel),
 // fp16 or bf16 q, D = 64 or 128, K packed INT4 with V's groups or (D = 128) INT8 with
 // one scale per row or V's groups, and at most two head sets of 16 rows.  The
 // per-head kernel covers INT4 K with one head set; the other shapes need the
@@ -1217,6 +1248,9 @@ bool mfma_supported(int group, int head_size, int k_format, int k_gs, int v_form
     if (k_gs != v_gs) return false;
   } else if (k_format == KNLP_KV_INT8_SYM) {
     if (head_size != 128 || (k_gs != head_size && k_gs != v_gs)) return false;
+  } else if (k_format == KNLP_KV_FP16) {
+    // fp16 K on the per-head kernel: INT4 V, one head set
+    return !v8 && group >= 1 && group * ng <= 16;
   } else {
     return false;
   }
@@ -1251,6 +1285,7 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const bool ka = a.kp.format == KNLP_KV_INT4_ASYM;
   const bool va = a.vp.format == KNLP_KV_INT4_ASYM;
   const bool v8 = a.vp.format == KNLP_KV_INT8_SYM;
+  const bool k16 = a.kp.format == KNLP_KV_FP16;
   const int nset = (a.group * ng + 15) / 16;
   const bool coop = coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
                     coop_layout_ok(a.vp, head_size, a.num_kv_heads);
@@ -1266,6 +1301,24 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   else if (ka) KNLP_LAUNCH(KERNEL<D, NG, true, false __VA_ARGS__>);                       \
   else if (va) KNLP_LAUNCH(KERNEL<D, NG, false, true __VA_ARGS__>);                       \
   else KNLP_LAUNCH(KERNEL<D, NG, false, false __VA_ARGS__>);
+  if (k16) {                       // fp16 K: per-head kernel, any kv-head count
+    const dim3 grid16(a.num_splits, a.num_seqs, a.num_kv_heads / heads_per_block_mfma(a.num_kv_heads));
+    const dim3 block16(kWave * heads_per_block_mfma(a.num_kv_heads));
+#define KNLP_K16(D, NG)                                                                   \
+    if (head_size == D && ng == NG) {                                                     \
+      if (va) hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, true, true>), grid16, block16, 0, stream, a); \
+      else hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, false, true>), grid16, block16, 0, stream, a); \
+      return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                 \
+    }
+    KNLP_K16(128, 4)
+    KNLP_K16(128, 2)
+    KNLP_K16(128, 1)
+    KNLP_K16(64, 4)
+    KNLP_K16(64, 2)
+    KNLP_K16(64, 1)
+#undef KNLP_K16
+    return KNLP_ERR_SHAPE;
+  }
 #define KNLP_INT4(D, NG)                                                                  \
   if (!k8 && !v8 && head_size == D && ng == NG) {                                         \
     if (coop && nset == 1) {                                                              \

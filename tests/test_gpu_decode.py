@@ -122,6 +122,10 @@ CASES = [
     ("kint8_row_vint8_g32_two_sets", [1100, 5, 33], 40, 8, 128, 2, 2, 128, 32),
     ("kint8_vint8_row", [640, 17], 32, 8, 128, 2, 2, 128, 128),
     ("kint8_vint8_hkv4_valu", [300], 16, 4, 128, 2, 2, 32, 32),
+    # fp16 K with INT4 V on the per-head matrix-core kernel
+    ("kfp16_vint4_sym_hkv4", [500, 17], 16, 4, 128, 3, 0, 128, 32),
+    ("kfp16_vint4_d64_g2", [300, 1], 16, 8, 64, 3, 1, 64, 32),
+    ("kfp16_vint4_row", [800], 32, 8, 128, 3, 1, 128, 128),
 ]
 
 
@@ -292,7 +296,8 @@ def test_kernel_kind_dispatch():
     assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT4_ASYM, 32) == "valu"
     assert kk(32, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT8_SYM, 32) == "mfma"
     assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT8_SYM, 32) == "valu"
-    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT4_ASYM, 32) == "valu"
+    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT4_ASYM, 32) == "mfma"
+    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT8_SYM, 32) == "valu"
 
 
 @pytest.mark.parametrize("kfmt,vfmt,hkv,hq", [(0, 1, 8, 32), (1, 0, 8, 40), (0, 1, 4, 16),
