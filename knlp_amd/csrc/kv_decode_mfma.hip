@@ -225,11 +225,13 @@ struct Codes<2> {
 
 // One 16-token sub-tile in the per-lane layout.  K: KCH code dwords and NGK
 // scale halves per row (packed INT4: KCH = NCH, NGK = NG; INT8: KCH = 2 NCH
-// and NGK scale groups, 1 for one scale per row); V: packed INT4.
-template <int NCH, int NG, int KCH = NCH, int NGK = NG>
+// and NGK scale groups, 1 for one scale per row; fp16: KCH = 4 NCH, no
+// scales); V: VCH code dwords (packed INT4: NCH, INT8: 2 NCH).
+template <int NCH, int NG, int KCH = NCH, int NGK = NG, int VCH = NCH>
 struct SubTile {
+  using VCodes = Codes<VCH>;
   Codes<KCH> k;
-  Codes<NCH> v;
+  Codes<VCH> v;
   Halves<NGK> ks;
   Halves<NG> kz, vs, vz;
 };
@@ -274,9 +276,9 @@ struct PageWindow {
   }
 };
 
-template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH>
+template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH, int VCH = NCH>
 __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane, int pbase,
-                                         SubTile<NCH, NG, KCH>& st) {
+                                         SubTile<NCH, NG, KCH, NG, VCH>& st) {
   const int64_t page = P.page(A.bt, lane, pbase >> A.bs_shift);
   const int64_t off0 = pbase & ((1 << A.bs_shift) - 1);
   st.k.load(rsrc_of(A.kc + (page * A.kc_b + off0 * A.kc_p)), A.lkc);
@@ -306,7 +308,7 @@ struct WaveState {
   static constexpr bool K8 = KCH == 2 * NCH;
   // fp16 K: four dwords of halves per QK chunk, used as they are (no scale)
   static constexpr bool K16 = KCH == 4 * NCH;
-  using ST = SubTile<NCH, NG, KCH, NGK>;
+  using ST = SubTile<NCH, NG, KCH, NGK, V8 ? 2 * NCH : NCH>;
   static constexpr bool KZ_USED = KASYM;
   static constexpr bool VZ_USED = VASYM;
   static_assert(NG % NGK == 0 && (K8 || K16 || NGK == NG),
@@ -446,13 +448,27 @@ struct WaveState {
 
   // PV with V transposed on the matrix cores (V arrives as lane = token):
   // accumulator (c, h) holds column d = (D/4)(col/4) + 8c + 2(col%4) + h.
+  // INT8 V (V8): the 8 bytes of chunk c, elements in the nibble order of
+  // nibbles_to_i8x8 ([e0 e2 e4 e6 | e1 e3 e5 e7]), go through the same
+  // transpose with the accumulator started at 128, so each output is the
+  // biased code n + 128: the fp16 subnormal (n + 128) 2^-24.
   __device__ __forceinline__ void pv_transposed(const ST (&st)[2], const h8& ahi,
                                                 const h8& alo) {
-    const i4 vzero = {0, 0, 0, 0};
+    const i4 vzero = V8 ? i4{128, 128, 128, 128} : i4{0, 0, 0, 0};
+    const auto v_i8 = [](const typename ST::VCodes& v, int c) -> long {
+      if constexpr (V8) {
+        const uint32_t w0 = v.dw(2 * c), w1 = v.dw(2 * c + 1);
+        const uint64_t lo = __builtin_amdgcn_perm(w1, w0, 0x06040200u);   // e0 e2 e4 e6
+        const uint64_t hi = __builtin_amdgcn_perm(w1, w0, 0x07050301u);   // e1 e3 e5 e7
+        return static_cast<long>(lo | (hi << 32));
+      } else {
+        return nibbles_to_i8x8(v.dw(c));
+      }
+    };
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const long va = nibbles_to_i8x8(st[0].v.dw(c));
-      const long vb = nibbles_to_i8x8(st[1].v.dw(c));
+      const long va = v_i8(st[0].v, c);
+      const long vb = v_i8(st[1].v, c);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const i4 ta = __builtin_amdgcn_mfma_i32_16x16x32_i8(va, vsel[h], vzero, 0, 0, 0);
@@ -721,11 +737,12 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
 
 // Per-head loads: each wave fetches its own kv head's rows (any layout that
 // passes the alignment checks).  One wave per (sequence, kv head, split).
-template <int D, int NG, bool KASYM, bool VASYM, bool K16 = false>
+template <int D, int NG, bool KASYM, bool VASYM, bool K16 = false, bool V8 = false>
 __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   constexpr int NCH = D / 32;    // K-chunks of 32 along head_dim = dwords per lane
   constexpr int LB = D / 8;      // bytes of INT4 codes per lane per token
   constexpr int KCH = K16 ? 4 * NCH : NCH;   // fp16 K: D/2 bytes per lane per token
+  constexpr int VCH = V8 ? 2 * NCH : NCH;    // INT8 V: D/4 bytes per lane per token
   constexpr int KEB = K16 ? 2 : 1;           // K element bytes (its strides are in elements)
   const int lane = threadIdx.x & (kWave - 1);
   const int col = lane & 15;
@@ -745,8 +762,8 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   // the token being decoded, when the caller fused its append into this launch
   decode_append<D>(a, seq, kvh, split, seq_len, lane);
 
-  WaveState<NCH, NG, KASYM, VASYM, KCH> W;
-  init_wave<D, NG, KASYM, VASYM, KCH>(W, a, seq, kvh, col, blk);
+  WaveState<NCH, NG, KASYM, VASYM, KCH, NG, V8> W;
+  init_wave<D, NG, KASYM, VASYM, KCH, NG, V8>(W, a, seq, kvh, col, blk);
 
   Addr A;
   {
@@ -767,7 +784,7 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
     // a lane holds elements 32 blk .. 32 blk + 31 of its token: D/8 bytes of
     // INT4 codes or D/2 bytes of fp16
     A.lkc = static_cast<uint32_t>(KEB * col * K.stride_page + (K16 ? D / 2 : LB) * blk);
-    A.lvc = static_cast<uint32_t>(col * V.stride_page + LB * blk);
+    A.lvc = static_cast<uint32_t>(col * V.stride_page + (V8 ? D / 4 : LB) * blk);
     A.lks = static_cast<uint32_t>(2 * col * K.s_stride_page);
     A.lvs = static_cast<uint32_t>(2 * col * V.s_stride_page);
     A.lkz = static_cast<uint32_t>(2 * col * K.z_stride_page);
@@ -785,13 +802,15 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   // can end in a partial tile; that one runs the masked step.  Tiles are
   // visited in increasing order so the page window only moves forward.
   const int ntiles = (t_end - t_begin + 31) / 32;
-  SubTile<NCH, NG, KCH> X[2], Y[2];
-  auto load_tile = [&](int tb, SubTile<NCH, NG, KCH>(&buf)[2]) {
-    load_sub<NCH, NG, KASYM, VASYM, KCH>(A, PW, lane, tb, buf[0]);
+  using ST = SubTile<NCH, NG, KCH, NG, VCH>;
+  ST X[2], Y[2];
+  auto load_tile = [&](int tb, ST(&buf)[2]) {
+    load_sub<NCH, NG, KASYM, VASYM, KCH, VCH>(A, PW, lane, tb, buf[0]);
     // a second half wholly past the end re-reads the first half's page (masked)
-    load_sub<NCH, NG, KASYM, VASYM, KCH>(A, PW, lane, tb + 16 < t_end ? tb + 16 : tb, buf[1]);
+    load_sub<NCH, NG, KASYM, VASYM, KCH, VCH>(A, PW, lane, tb + 16 < t_end ? tb + 16 : tb,
+                                              buf[1]);
   };
-  auto run_tile = [&](int tb, const SubTile<NCH, NG, KCH>(&buf)[2]) {
+  auto run_tile = [&](int tb, const ST(&buf)[2]) {
     if (tb + 32 <= t_end)
       W.template step<false>(buf, tb, t_end, col);
     else
@@ -806,7 +825,7 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
     if (i + 2 < ntiles) load_tile(tb + 64, X);
     run_tile(tb + 32, Y);
   }
-  write_partials<D, NG, KASYM, VASYM, false, KCH>(W, a, seq, kvh, split, col, blk);
+  write_partials<D, NG, KASYM, VASYM, false, KCH, NG, V8>(W, a, seq, kvh, split, col, blk);
 }
 
 // ---------------------------------------------------------------------------
@@ -988,9 +1007,9 @@ __device__ __forceinline__ void halves_from_lds(Halves<NG>& h, const uint8_t* p)
 // This wave's head slice of the tile in `buf`, in the per-head lane layout:
 // each lane holds a quarter of its token's K row (D/8 bytes of INT4 codes or
 // D/4 bytes of INT8 codes) and the token's scale / zero halves.
-template <class L, bool KASYM, bool VASYM, int NCH, int NG, int KCH, int NGK>
+template <class L, bool KASYM, bool VASYM, int NCH, int NG, int KCH, int NGK, int VCH>
 __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col, int blk,
-                                          SubTile<NCH, NG, KCH, NGK> (&st)[2]) {
+                                          SubTile<NCH, NG, KCH, NGK, VCH> (&st)[2]) {
   constexpr int KLB = L::HBK / 4;    // K code bytes per lane and token
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
@@ -1226,8 +1245,8 @@ int heads_per_block_mfma(int num_kv_heads) {
 }  // namespace
 
 // Shapes the matrix-core path takes: INT4 V with 1, 2 or 4 scale groups
-// (or, at D = 128, INT8 V with 1 or 4; or fp16 K with INT4 V and one head
-// set, on the per-head kernel),
+// (or, at D = 128, INT8 V with 1 or 4; or fp16 K with INT4 or INT8 V and one
+// head set, on the per-head kernel),
 // fp16 or bf16 q, D = 64 or 128, K packed INT4 with V's groups or (D = 128) INT8 with
 // one scale per row or V's groups, and at most two head sets of 16 rows.  The
 // per-head kernel covers INT4 K with one head set; the other shapes need the
@@ -1249,8 +1268,8 @@ bool mfma_supported(int group, int head_size, int k_format, int k_gs, int v_form
   } else if (k_format == KNLP_KV_INT8_SYM) {
     if (head_size != 128 || (k_gs != head_size && k_gs != v_gs)) return false;
   } else if (k_format == KNLP_KV_FP16) {
-    // fp16 K on the per-head kernel: INT4 V, one head set
-    return !v8 && group >= 1 && group * ng <= 16;
+    // fp16 K on the per-head kernel: INT4 or INT8 V, one head set
+    return group >= 1 && group * ng <= 16;
   } else {
     return false;
   }
@@ -1289,7 +1308,9 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const int nset = (a.group * ng + 15) / 16;
   const bool coop = coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
                     coop_layout_ok(a.vp, head_size, a.num_kv_heads);
-  if (!coop && (k8 || v8 || nset > 1))     // only the cooperative kernel has these
+  // only the cooperative kernel has these (the per-head kernel takes INT8 V
+  // with fp16 K only)
+  if (!coop && (k8 || (v8 && !k16) || nset > 1))
     return launch_decode_valu(a, head_size, heads_per_block_mfma(a.num_kv_heads), stream);
   const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
   const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
@@ -1305,10 +1326,18 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
     const dim3 grid16(a.num_splits, a.num_seqs, a.num_kv_heads / heads_per_block_mfma(a.num_kv_heads));
     const dim3 block16(kWave * heads_per_block_mfma(a.num_kv_heads));
 #define KNLP_K16(D, NG)                                                                   \
-    if (head_size == D && ng == NG) {                                                     \
+    if (head_size == D && ng == NG && !v8) {                                              \
       if (va) hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, true, true>), grid16, block16, 0, stream, a); \
       else hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, false, true>), grid16, block16, 0, stream, a); \
       return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                 \
+    }
+    if (v8 && head_size == 128 && ng == 4) {
+      hipLaunchKernelGGL((decode_mfma_kernel<128, 4, false, false, true, true>), grid16, block16, 0, stream, a);
+      return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
+    }
+    if (v8 && head_size == 128 && ng == 1) {
+      hipLaunchKernelGGL((decode_mfma_kernel<128, 1, false, false, true, true>), grid16, block16, 0, stream, a);
+      return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
     }
     KNLP_K16(128, 4)
     KNLP_K16(128, 2)

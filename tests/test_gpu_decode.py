@@ -126,6 +126,8 @@ CASES = [
     ("kfp16_vint4_sym_hkv4", [500, 17], 16, 4, 128, 3, 0, 128, 32),
     ("kfp16_vint4_d64_g2", [300, 1], 16, 8, 64, 3, 1, 64, 32),
     ("kfp16_vint4_row", [800], 32, 8, 128, 3, 1, 128, 128),
+    ("kfp16_vint8_row", [700, 3], 32, 8, 128, 3, 2, 128, 128),
+    ("kfp16_vint8_hkv4", [450, 33], 16, 4, 128, 3, 2, 128, 32),
 ]
 
 
@@ -297,7 +299,8 @@ def test_kernel_kind_dispatch():
     assert kk(32, 8, 128, _lib.KV_INT8_SYM, 128, _lib.KV_INT8_SYM, 32) == "mfma"
     assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT8_SYM, 32) == "valu"
     assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT4_ASYM, 32) == "mfma"
-    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT8_SYM, 32) == "valu"
+    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT8_SYM, 32) == "mfma"
+    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_FP16, 128) == "valu"
 
 
 @pytest.mark.parametrize("kfmt,vfmt,hkv,hq", [(0, 1, 8, 32), (1, 0, 8, 40), (0, 1, 4, 16),
