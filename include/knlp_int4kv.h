@@ -70,7 +70,9 @@ typedef struct knlp_kv_plane {
   int64_t s_stride_block, s_stride_page, s_stride_head;
   int64_t z_stride_block, z_stride_page, z_stride_head;
   int32_t format;           /* enum knlp_kv_format */
-  int32_t group_size;       /* elements per scale group along head_dim */
+  int32_t group_size;       /* elements per scale group along head_dim; not
+                               read for KNLP_KV_FP16 planes (no scales: any
+                               value, 0 included, is taken as head_size) */
 } knlp_kv_plane;
 
 int knlp_abi_version(void);
@@ -97,14 +99,32 @@ int knlp_kv_append(const void* key, const void* value, int32_t src_dtype,
 /*
  * Split-K plan: tokens per split for a batch whose longest possible context
  * is max_context (= block-table width * block_size; no device read-back),
- * for K/V planes of the given knlp_kv_format values (the kernel that will
- * run decides how many workgroups a CU holds).  Returns the split length in
- * tokens (> 0) or a negative status.
+ * for K/V planes of the given knlp_kv_format values, taking one scale per
+ * row for INT8 planes and group size 32 for INT4 planes (the reference's
+ * default GROUP_SIZE, F:55); knlp_kv_decode_plan takes the group sizes and
+ * the batch's total context.  Returns the split length in tokens (> 0) or a
+ * negative status.
  */
 int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads,
                                     int32_t num_q_heads, int32_t head_size,
                                     int32_t max_context, int32_t k_format,
                                     int32_t v_format);
+
+/*
+ * Split-K plan with everything the dispatch looks at: group sizes decide
+ * which decode kernel runs (and so how many workgroups a CU holds), and
+ * total_context -- the sum of the batch's sequence lengths, when the caller
+ * knows it on the host (vLLM's metadata does) -- sizes the splits of a
+ * variable-length batch from its real work; total_context <= 0 means
+ * unknown (every sequence taken at max_context).  Returns the split length
+ * in tokens (> 0, a multiple of 64) or a negative status.  No counterpart
+ * in the reference (it has no split-K).
+ */
+int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads,
+                            int32_t num_q_heads, int32_t head_size,
+                            int32_t max_context, int64_t total_context,
+                            int32_t k_format, int32_t k_group_size,
+                            int32_t v_format, int32_t v_group_size);
 
 /* Bytes of fp32 workspace decode needs for this shape and split length. */
 int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
@@ -210,10 +230,12 @@ int knlp_int4_twos_to_offset(const void* src, int64_t src_stride_row, void* dst,
 
 /* Which decode kernel a shape dispatches to: 1 = MFMA path, 0 = VALU path,
  * negative = unsupported (status).  Lets tests and the bench report it.  The
- * MFMA path's INT8-K and more-than-16-row shapes need densely packed heads
- * (stride_head = one head's row) and num_kv_heads % 8 == 0; other layouts of
- * those shapes run on the VALU kernel, which serves at most 8 query heads per
- * kv head (more return KNLP_ERR_SHAPE at decode time). */
+ * MFMA path's INT8-K, INT8-V (with INT4 or INT8 K) and more-than-16-row
+ * shapes need num_kv_heads % 8 == 0 (reported as 0 otherwise) and densely
+ * packed heads (stride_head = one head's row, assumed here); other layouts
+ * of those shapes run on the VALU kernel, which serves at most 8 query heads
+ * per kv head (more return KNLP_ERR_SHAPE at decode time).  Group sizes of
+ * fp16 planes are not read. */
 int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads,
                                int32_t head_size, int32_t k_format,
                                int32_t k_group_size, int32_t v_format,

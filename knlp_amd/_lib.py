@@ -23,7 +23,7 @@ KV_INT4_SYM, KV_INT4_ASYM, KV_INT8_SYM, KV_FP16 = 0, 1, 2, 3
 
 EXPORTS = (
     "knlp_abi_version", "knlp_status_string", "knlp_kv_append",
-    "knlp_kv_decode_split_tokens", "knlp_kv_decode_workspace_bytes",
+    "knlp_kv_decode_split_tokens", "knlp_kv_decode_plan", "knlp_kv_decode_workspace_bytes",
     "knlp_kv_decode_partial", "knlp_kv_decode_merge", "knlp_kv_decode",
     "knlp_kv_decode_kernel_kind", "knlp_kv_append_decode", "knlp_int4_twos_to_offset",
 )
@@ -58,6 +58,7 @@ _SIGS = {
     "knlp_kv_append": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I64, _I64, _I64, _I64,
                               _PLANE, _PLANE, _P, _I32, _I32, _F, _P]),
     "knlp_kv_decode_split_tokens": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
+    "knlp_kv_decode_plan": (_I32, [_I32, _I32, _I32, _I32, _I32, _I64, _I32, _I32, _I32, _I32]),
     "knlp_kv_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
     "knlp_kv_decode_partial": (_I32, [_P, _I32, _I64, _I64, _I32, _I32, _I32, _I32,
                                       _PLANE, _PLANE, _P, _I64, _P, _I32, _I32, _F, _I32,

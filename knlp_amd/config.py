@@ -25,3 +25,9 @@ DECODE_GATHERED_SCALE: bool = os.environ.get(
     "VLLM_FUSED_INT4_DECODE_GATHERED_SCALE", "0") == "1"
 # Split length override for the split-K decode (0 = library plan).
 DECODE_SPLIT_TOKENS: int = int(os.environ.get("KNLP_DECODE_SPLIT_TOKENS", "0"))
+# Softmax scale of the backend's fused decode.  The reference's fused
+# kernels fix it to 1/sqrt(head_size) (F:924) whatever scale the layer was
+# built with (its _fused_decode, F:2851-2928, passes none), and so does this
+# package by default.  Set to 1 to use the layer's own scale instead (models
+# whose attention scale is not 1/sqrt(head_size)).
+FUSED_DECODE_LAYER_SCALE: bool = os.environ.get("KNLP_FUSED_DECODE_LAYER_SCALE", "0") == "1"

@@ -74,6 +74,18 @@ bool mfma_layout_ok(const knlp_kv_plane& P, int head_size, int block_size) {
   return true;
 }
 
+// Largest grid y / z extent of a HIP launch; the decode and merge launches
+// put the sequences on y.
+constexpr int kMaxGridYZ = 65535;
+
+// A copy of a plane in which an fp16 plane's group_size (a field it does not
+// use: it has no scales) reads head_size, so no later division sees 0.
+knlp_kv_plane fp16_groups_as_rows(const knlp_kv_plane& P, int head_size) {
+  knlp_kv_plane Q = P;
+  if (Q.format == KNLP_KV_FP16) Q.group_size = head_size;
+  return Q;
+}
+
 int check_head_size(int head_size) {
   return (head_size == 32 || head_size == 64 || head_size == 128 || head_size == 256)
              ? KNLP_OK
@@ -156,35 +168,48 @@ int knlp_kv_append(const void* key, const void* value, int32_t src_dtype, int64_
                        block_size, clip_ratio, static_cast<hipStream_t>(stream));
 }
 
-int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads, int32_t num_q_heads,
-                                    int32_t head_size, int32_t max_context, int32_t k_format,
-                                    int32_t v_format) {
-  if (num_seqs <= 0 || num_kv_heads <= 0 || max_context <= 0 || head_size <= 0)
+int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads, int32_t num_q_heads,
+                            int32_t head_size, int32_t max_context, int64_t total_context,
+                            int32_t k_format, int32_t k_group_size, int32_t v_format,
+                            int32_t v_group_size) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || max_context <= 0 || head_size <= 0 ||
+      num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return KNLP_ERR_SHAPE;
-  (void)num_q_heads;
-  // Aim for about two resident workgroups per CU over the whole batch (one
-  // for the cooperative matrix-core kernel -- INT4 or INT8 codes (INT8 at
-  // D = 128), Hkv % 8 == 0 -- which runs one 8-wave block per CU holding 100-160 KB
-  // of LDS tile buffers, so that every block starts in the first round), in
-  // multiples of 64 tokens.  Small batches get short splits down to 64
-  // tokens (config 1, one 1024-token sequence: 9.6 us per step at 64 tokens
-  // against 17 us at 256); partials cost (D+2)*4 bytes per q head and split
-  // on each side of the merge, negligible at that size.
-  const auto int4 = [](int f) { return f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM; };
-  const auto int8_128 = [&](int f) { return f == KNLP_KV_INT8_SYM && head_size == 128; };
-  const bool wide = num_kv_heads % 8 == 0 && (int4(v_format) || int8_128(v_format)) &&
-                    (int4(k_format) || int8_128(k_format));
+  // Aim for about two resident workgroups per CU over the whole batch, or one
+  // when the cooperative matrix-core kernel will run (it holds one 8-wave
+  // block per CU with 100-160 KB of LDS tile buffers, so every block starts in
+  // the first round), in multiples of 64 tokens.  Small batches get short
+  // splits down to 64 tokens (config 1, one 1024-token sequence: 9.6 us per
+  // step at 64 tokens against 17 us at 256); partials cost (D+2)*4 bytes per
+  // q head and split on each side of the merge, negligible at that size.
+  const int g = num_q_heads / num_kv_heads;
+  const bool wide = num_kv_heads % 8 == 0 && k_format != KNLP_KV_FP16 &&
+                    mfma_supported(g, head_size, k_format,
+                                   k_format == KNLP_KV_FP16 ? head_size : k_group_size, v_format,
+                                   v_format == KNLP_KV_FP16 ? head_size : v_group_size, 0);
   const int hpb = wide ? 8 : heads_per_block(num_kv_heads);
-  const int64_t groups =
-      static_cast<int64_t>(num_seqs) * ((num_kv_heads + hpb - 1) / hpb);
+  const int64_t hgroups = (num_kv_heads + hpb - 1) / hpb;
   const int64_t target = (wide ? 1LL : 2LL) * num_cus();
-  int64_t splits = (target + groups - 1) / groups;
-  if (splits < 1) splits = 1;
-  int64_t tok = (max_context + splits - 1) / splits;
+  // tokens over all sequences: the caller's host-side total when it has one
+  // (variable-length batches), else every sequence at max_context
+  const int64_t total =
+      total_context > 0 ? total_context : static_cast<int64_t>(num_seqs) * max_context;
+  int64_t tok = (total * hgroups + target - 1) / target;
   if (tok < 64) tok = 64;
   tok = (tok + 63) / 64 * 64;
   if (tok > max_context) tok = (static_cast<int64_t>(max_context) + 63) / 64 * 64;
   return static_cast<int32_t>(tok);
+}
+
+int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads, int32_t num_q_heads,
+                                    int32_t head_size, int32_t max_context, int32_t k_format,
+                                    int32_t v_format) {
+  // group sizes this entry point does not take: one scale per row for INT8,
+  // 32 (the reference's default GROUP_SIZE, F:55) for INT4
+  const auto gs = [&](int f) { return f == KNLP_KV_INT8_SYM ? head_size : 32; };
+  if (num_q_heads <= 0) num_q_heads = num_kv_heads;
+  return knlp_kv_decode_plan(num_seqs, num_kv_heads, num_q_heads, head_size, max_context, 0,
+                             k_format, gs(k_format), v_format, gs(v_format));
 }
 
 int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t head_size,
@@ -202,8 +227,15 @@ int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads, int32_
   if (num_kv_heads <= 0 || num_q_heads % num_kv_heads) return KNLP_ERR_SHAPE;
   const int g = num_q_heads / num_kv_heads;
   if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
-  const bool mfma = mfma_supported(g, head_size, k_format, k_group_size, v_format,
-                                   v_group_size, q_dtype == KNLP_DT_BF16);
+  bool mfma = mfma_supported(g, head_size, k_format, k_group_size, v_format, v_group_size,
+                             q_dtype == KNLP_DT_BF16);
+  // INT8 K, INT8 V (with INT4 / INT8 K) and two head sets exist only on the
+  // cooperative kernel, which takes 8 kv heads per block
+  const int vng = v_group_size > 0 ? head_size / v_group_size : 1;
+  const bool coop_only = k_format == KNLP_KV_INT8_SYM ||
+                         (v_format == KNLP_KV_INT8_SYM && k_format != KNLP_KV_FP16) ||
+                         g * vng > 16;
+  if (mfma && coop_only && num_kv_heads % 8 != 0) mfma = false;
   // the VALU kernel serves up to 8 query heads per kv head; the matrix-core
   // kernel up to two 16-row head sets (on dense cache layouts)
   if (g > 8 && !mfma) return KNLP_ERR_SHAPE;
@@ -228,18 +260,19 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
       max_context <= 0 || split_tokens <= 0 || split_tokens % 64)
     return KNLP_ERR_SHAPE;
   if (num_seqs == 0) return KNLP_OK;   // empty tensors may carry null data pointers
+  if (num_seqs > kMaxGridYZ) return KNLP_ERR_SHAPE;   // one grid row per sequence
   if (query == nullptr || block_table == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
   if (num_q_heads % num_kv_heads) return KNLP_ERR_SHAPE;
-  const int kind = knlp_kv_decode_kernel_kind(num_q_heads, num_kv_heads, head_size,
-                                              key_cache ? key_cache->format : -1,
-                                              key_cache ? key_cache->group_size : 0,
-                                              value_cache ? value_cache->format : -1,
-                                              value_cache ? value_cache->group_size : 0,
-                                              q_dtype);
+  if (key_cache == nullptr || value_cache == nullptr) return KNLP_ERR_ARG;
+  // an fp16 plane has no scale groups: its group_size field is not read
+  const knlp_kv_plane kp = fp16_groups_as_rows(*key_cache, head_size);
+  const knlp_kv_plane vp = fp16_groups_as_rows(*value_cache, head_size);
+  const int kind = knlp_kv_decode_kernel_kind(num_q_heads, num_kv_heads, head_size, kp.format,
+                                              kp.group_size, vp.format, vp.group_size, q_dtype);
   if (kind < 0) return kind;
   int st;
-  if ((st = check_plane(key_cache, head_size, true))) return st;
-  if ((st = check_plane(value_cache, head_size, true))) return st;
+  if ((st = check_plane(&kp, head_size, true))) return st;
+  if ((st = check_plane(&vp, head_size, true))) return st;
   if (!std::isfinite(softmax_scale)) return KNLP_ERR_ARG;
   if (!aligned(query, 16) || q_stride_seq % 8 || q_stride_head % 8) return KNLP_ERR_ALIGN;
   const int ns = (max_context + split_tokens - 1) / split_tokens;
@@ -257,8 +290,8 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
-  a.kp = *key_cache;
-  a.vp = *value_cache;
+  a.kp = kp;
+  a.vp = vp;
   a.block_table = block_table;
   a.bt_stride = bt_stride_seq;
   a.seq_lens = seq_lens;
@@ -271,8 +304,8 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
   workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
   if (app != nullptr) a.app = *app;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kind == 1 && softmax_scale > 0.0f && mfma_layout_ok(*key_cache, head_size, block_size) &&
-      mfma_layout_ok(*value_cache, head_size, block_size))
+  if (kind == 1 && softmax_scale > 0.0f && mfma_layout_ok(kp, head_size, block_size) &&
+      mfma_layout_ok(vp, head_size, block_size))
     return launch_decode_mfma(a, head_size, s);
   return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), s);
 }
@@ -304,6 +337,7 @@ int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const i
     return KNLP_ERR_SHAPE;
   if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
   if (num_seqs == 0) return KNLP_OK;
+  if (num_seqs > kMaxGridYZ) return KNLP_ERR_SHAPE;
   if (out == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
   if (!aligned(out, 2)) return KNLP_ERR_ALIGN;
   const int ns = (max_context + split_tokens - 1) / split_tokens;

@@ -174,7 +174,8 @@ def reshape_and_cache_fp16(key, value, key_cache, value_cache, slot_mapping) -> 
 
 
 def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, num_kv_heads,
-            head_size, scale=None, split_tokens=None, append=None) -> torch.Tensor:
+            head_size, scale=None, split_tokens=None, append=None,
+            total_context=0) -> torch.Tensor:
     _require_cuda(query, block_table, seq_lens)
     if query.dtype not in _SRC_DTYPES:
         raise ValueError(f"query dtype {query.dtype} not supported (fp16 or bf16)")
@@ -194,9 +195,10 @@ def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, 
     L = lib()
     max_context = block_table.shape[1] * block_size
     if split_tokens is None:
-        split_tokens = config.DECODE_SPLIT_TOKENS or L.knlp_kv_decode_split_tokens(
-            num_seqs, num_kv_heads, num_heads, head_size, max_context, kp.format, vp.format)
-        check(split_tokens, "knlp_kv_decode_split_tokens")
+        split_tokens = config.DECODE_SPLIT_TOKENS or L.knlp_kv_decode_plan(
+            num_seqs, num_kv_heads, num_heads, head_size, max_context, int(total_context),
+            kp.format, kp.group_size, vp.format, vp.group_size)
+        check(split_tokens, "knlp_kv_decode_plan")
     ws_bytes = L.knlp_kv_decode_workspace_bytes(max(num_seqs, 1), num_heads, head_size,
                                                 max_context, split_tokens)
     check(ws_bytes, "knlp_kv_decode_workspace_bytes")

@@ -345,12 +345,18 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
         return output
 
     # ---- decode kernels -------------------------------------------------------------------
+    def _fused_scale(self) -> float | None:
+        """Softmax scale of the fused decode: None (1/sqrt(head_size), as the
+        reference's kernels fix it, F:924 with F:2851-2928 passing no scale)
+        unless KNLP_FUSED_DECODE_LAYER_SCALE=1 asks for the layer's scale."""
+        return self.scale if config.FUSED_DECODE_LAYER_SCALE else None
+
     def _fused_decode(self, q: torch.Tensor, key_cache_fp16: torch.Tensor,
                       block_table: torch.Tensor, seq_lens: torch.Tensor) -> torch.Tensor:
         """Dispatch on (k_precision, v_precision) (F:2845-2928)."""
         c, kp, vp = self._caches, self._k_precision, self._v_precision
         common = dict(num_kv_heads=self.num_kv_heads, head_size=self.head_size,
-                      scale=self.scale)
+                      scale=self._fused_scale())
         if kp == "fp16" and vp == "int8":
             return ops.kfp16_vint8_decode(q, key_cache_fp16, c.int8_value, c.v_int8_scales,
                                           block_table, seq_lens, **common)
@@ -388,7 +394,7 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
         return ops.append_and_decode(
             q, key, value_3d[:n], md.slot_mapping[:n], kcache, vcache, ks, vs, md.block_table,
             md.seq_lens, self.num_kv_heads, self.head_size, k_format=kp, v_format=vp,
-            k_zeros=kz, v_zeros=vz, asymmetric=asym, scale=self.scale)
+            k_zeros=kz, v_zeros=vz, asymmetric=asym, scale=self._fused_scale())
 
     def _paged_decode(self, q, key_cache, value_cache, block_table, seq_lens) -> torch.Tensor:
         """Short sequences from the fp16 paged cache (F:2930-3048)."""

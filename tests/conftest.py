@@ -28,3 +28,18 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Achieved max-abs error of every parity check against the oracle."""
+    try:
+        from tests import tolerance
+    except ImportError:
+        return
+    if not tolerance.RESULTS:
+        return
+    terminalreporter.write_sep("-", "decode parity: achieved max-abs error vs oracle (bar 2e-3)")
+    worst = max(tolerance.RESULTS, key=lambda r: r[1])
+    for name, err, mx in tolerance.RESULTS:
+        terminalreporter.write_line(f"{err:9.3e}  (max |ref| {mx:8.3g})  {name}")
+    terminalreporter.write_line(f"worst: {worst[1]:.3e} in {worst[0]}")

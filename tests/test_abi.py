@@ -113,3 +113,58 @@ def test_ops_require_device_tensors():
     with pytest.raises(ValueError):
         ops.fused_int4_decode(q, kc, kc, sc, sc, torch.zeros(1, 2, dtype=torch.int32),
                               torch.ones(1, dtype=torch.int32), 1, 64)
+
+
+def test_fp16_plane_group_size_is_not_read():
+    """An fp16 plane has no scales; a group_size of 0 in it must not reach a
+    division (it used to end the process with SIGFPE on the dispatch path).
+    Without a GPU the call gets as far as the launch and reports that."""
+    L = _lib.lib()
+    kp = _plane(fmt=_lib.KV_FP16, gs=0, scales=None, zeros=None)
+    kp.stride_block, kp.stride_page, kp.stride_head = 16 * 8 * 128, 8 * 128, 128
+    for vfmt, vgs in ((_lib.KV_INT4_ASYM, 32), (_lib.KV_INT8_SYM, 32), (_lib.KV_FP16, 0)):
+        vp = _plane(fmt=vfmt, gs=vgs) if vfmt != _lib.KV_FP16 else \
+            _plane(fmt=_lib.KV_FP16, gs=0, scales=None, zeros=None)
+        if vfmt == _lib.KV_FP16:
+            vp.stride_block, vp.stride_page, vp.stride_head = 16 * 8 * 128, 8 * 128, 128
+        if vfmt == _lib.KV_INT8_SYM:
+            vp.stride_block, vp.stride_page, vp.stride_head = 16 * 8 * 128, 8 * 128, 128
+        st = L.knlp_kv_decode(0x10000, _lib.DT_F16, 32 * 128, 128, 8, 32, 8, 128,
+                              ctypes.byref(kp), ctypes.byref(vp), 0x50000, 2048, 0x60000, 16,
+                              32768, 0.088, 1024, 0x100000, 1 << 40, 0x70000, _lib.DT_F16,
+                              32 * 128, 128, None)
+        assert st in (_lib.OK, _lib.ERR_LAUNCH)
+        assert L.knlp_kv_decode_kernel_kind(32, 8, 128, _lib.KV_FP16, 0, vfmt, vgs, 0) in (0, 1)
+
+
+def test_grid_limits_return_shape_errors():
+    """More sequences than a launch grid row holds (65535) is a shape error,
+    not a failed launch."""
+    L = _lib.lib()
+    kp, vp = _plane(), _plane()
+    st = L.knlp_kv_decode(0x10000, _lib.DT_F16, 32 * 128, 128, 70000, 32, 8, 128,
+                          ctypes.byref(kp), ctypes.byref(vp), 0x50000, 2048, 0x60000, 16,
+                          32768, 0.088, 1024, 0x100000, 1 << 40, 0x70000, _lib.DT_F16,
+                          32 * 128, 128, None)
+    assert st == _lib.ERR_SHAPE
+    st = L.knlp_kv_decode_merge(0x100000, 1 << 40, 0x60000, 70000, 32, 128, 32768, 1024,
+                                0x70000, _lib.DT_F16, 32 * 128, 128, None)
+    assert st == _lib.ERR_SHAPE
+
+
+def test_decode_plan_uses_group_sizes_and_total_context():
+    L = _lib.lib()
+    a4, i8 = _lib.KV_INT4_ASYM, _lib.KV_INT8_SYM
+    legacy = L.knlp_kv_decode_split_tokens(8, 8, 32, 128, 32768, a4, a4)
+    assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, a4, 32, a4, 32) == legacy
+    assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 8 * 32768, a4, 32, a4, 32) == legacy
+    # a variable-length batch with half the tokens of its rectangle: shorter splits
+    var = L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 64 * 8192, a4, 32, a4, 32)
+    full = L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 0, a4, 32, a4, 32)
+    assert 64 <= var < full and var % 64 == 0
+    # INT8 V with g64 runs on the VALU kernel (two workgroups per CU): half
+    # the split length of the cooperative kernel's plan for the same shape
+    coop = L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, i8, 128, i8, 128)
+    valu = L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, i8, 128, i8, 64)
+    assert valu < coop
+    assert L.knlp_kv_decode_plan(8, 7, 32, 128, 32768, 0, a4, 32, a4, 32) == _lib.ERR_SHAPE

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import attention as A
-from tests import kvgen
+from tests import tolerance, kvgen
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "int4kv_golden.npz")
 APPEND = (("asym", 1, 0.0), ("sym", 0, 10.0), ("int8", 2, 0.0))
@@ -89,4 +89,4 @@ def test_hip_decode_matches_fixture(z):
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     ref = z["decode_out_f32"]
-    assert np.all(np.abs(got - ref) <= 2e-3 + 2.0 ** -10 * np.abs(ref))
+    tolerance.check("golden_decode", got, ref)

@@ -17,15 +17,26 @@ pytestmark = pytest.mark.gpu
 BS = 16
 
 CASES = [
-    # name, seq_lens (incl. the new token), hq, hkv, d, kfmt, vfmt, kgs, vgs, split, src dtype
-    ("coop_int4_asym", [1, 33, 1024, 2049], 32, 8, 128, 1, 1, 32, 32, 1024, torch.float16),
-    ("coop_int4_sym_split_edge", [257, 512, 513], 32, 8, 128, 0, 0, 32, 32, 256, torch.float16),
-    ("perhead_mfma_hkv4", [700, 65], 16, 4, 128, 1, 1, 32, 32, 256, torch.float16),
-    ("mfma_d64", [300, 1], 16, 8, 64, 1, 1, 32, 32, 256, torch.float16),
-    ("valu_kint8_vint4", [900, 17], 40, 8, 128, 2, 1, 128, 32, 256, torch.float16),
-    ("valu_kfp16_vint8", [400], 32, 8, 128, 3, 2, 128, 32, 256, torch.float16),
-    ("valu_d256", [333, 32], 64, 8, 256, 1, 1, 32, 32, 256, torch.float16),
-    ("bf16_rows_int4", [600, 90], 32, 8, 128, 1, 1, 32, 32, 256, torch.bfloat16),
+    # name, seq_lens (incl. the new token), hq, hkv, d, kfmt, vfmt, kgs, vgs, split, src
+    # dtype, kernel kind the shape dispatches to
+    ("coop_int4_asym", [1, 33, 1024, 2049], 32, 8, 128, 1, 1, 32, 32, 1024, torch.float16,
+     "mfma"),
+    ("coop_int4_sym_split_edge", [257, 512, 513], 32, 8, 128, 0, 0, 32, 32, 256, torch.float16,
+     "mfma"),
+    ("perhead_mfma_hkv4", [700, 65], 16, 4, 128, 1, 1, 32, 32, 256, torch.float16, "mfma"),
+    ("mfma_d64", [300, 1], 16, 8, 64, 1, 1, 32, 32, 256, torch.float16, "mfma"),
+    ("coop_kint8_row_vint4_two_sets", [900, 17], 40, 8, 128, 2, 1, 128, 32, 256,
+     torch.float16, "mfma"),
+    ("perhead_kfp16_vint8", [400], 32, 8, 128, 3, 2, 128, 32, 256, torch.float16, "mfma"),
+    ("coop_kint8_vint8", [700, 33, 1], 32, 8, 128, 2, 2, 128, 32, 256, torch.float16, "mfma"),
+    ("coop_kint4_vint8", [512, 64], 32, 8, 128, 1, 2, 32, 32, 256, torch.float16, "mfma"),
+    ("valu_kint8_vint4_hkv4", [300, 48], 16, 4, 128, 2, 1, 128, 32, 256, torch.float16,
+     "valu"),
+    ("valu_kint8_vint8_hkv4", [300, 48], 16, 4, 128, 2, 2, 32, 32, 256, torch.float16,
+     "valu"),
+    ("valu_kint8_g64_vint8", [420], 32, 8, 128, 2, 2, 64, 64, 256, torch.float16, "valu"),
+    ("valu_d256", [333, 32], 64, 8, 256, 1, 1, 32, 32, 256, torch.float16, "valu"),
+    ("bf16_rows_int4", [600, 90], 32, 8, 128, 1, 1, 32, 32, 256, torch.bfloat16, "mfma"),
 ]
 
 
@@ -46,8 +57,11 @@ def _clone(t):
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_fused_append_matches_separate_launches(case):
-    name, seq_lens, hq, hkv, d, kf, vf, kgs, vgs, split, sdt = case
+    name, seq_lens, hq, hkv, d, kf, vf, kgs, vgs, split, sdt, kind = case
     dev = torch.device("cuda")
+    # the kernel family this case covers (kernel_kind reports the shape's
+    # kernel; Hkv % 8 != 0 or INT8 with two different groups fall back to VALU)
+    assert K.decode_kernel_kind(hq, hkv, d, kf, kgs, vf, vgs) == kind, name
     if sdt == torch.bfloat16 and 3 in (kf, vf):
         pytest.skip("fp16 caches take fp16 rows")
     nb = sum(-(-n // BS) for n in seq_lens) + 2

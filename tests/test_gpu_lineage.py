@@ -10,7 +10,7 @@ import torch
 import knlp_amd as K
 from oracle import attention as A
 from oracle import lineage as LN
-from tests import kvgen
+from tests import tolerance, kvgen
 
 pytestmark = pytest.mark.gpu
 
@@ -79,4 +79,4 @@ def test_gpt2_format_caches_decode(hkv):
         vv = torch.from_numpy(A.gather_sequence(vdeq, bt[s], n_s))
         ref[s] = A.sdpa_decode_f32(q[s].float(), kk, vv, float(np.float32(d ** -0.5))).numpy()
     got = out.float().cpu().numpy()
-    assert np.all(np.abs(got - ref) <= 2e-3 + 2.0 ** -10 * np.abs(ref))
+    tolerance.check("lineage_decode", got, ref)

@@ -18,20 +18,18 @@ import torch
 
 from knlp_amd import config, kv_layout
 from oracle import attention as A
-from tests import kvgen
+from tests import kvgen, tolerance
 
 pytestmark = pytest.mark.gpu
 
 STUB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "vllm_stub")
 H, HKV, D, BS, NB = 16, 4, 128, 16, 40
-# decode parity bar: max-abs 2e-3 against the fp32 oracle, plus the fp16
-# output rounding (an fp16 ulp, relative 2^-10) for large outputs
-ATOL, RTOL = 2e-3, 2.0 ** -10
-
-
-def close(got, ref, atol=ATOL, rtol=RTOL):
-    err = np.abs(got - ref)
-    return bool(np.isfinite(got).all() and (err <= atol + rtol * np.abs(ref)).all())
+def close(got, ref, bf16=False):
+    """The decode parity bar of tests/tolerance.py (asserts; records the
+    achieved error under the current test's name)."""
+    name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0].split("::")[-1]
+    tolerance.check(name, got, ref, bf16=bf16)
+    return True
 
 
 @pytest.fixture(scope="module")
@@ -46,13 +44,13 @@ def vb():
     return vb
 
 
-def impl_for(vb, monkeypatch, k="int4", v="int4", asym=True, msl=48):
+def impl_for(vb, monkeypatch, k="int4", v="int4", asym=True, msl=48, scale=D ** -0.5):
     monkeypatch.setattr(config, "K_PRECISION", k)
     monkeypatch.setattr(config, "V_PRECISION", v)
     monkeypatch.setattr(config, "ASYMMETRIC", asym)
     monkeypatch.setattr(config, "MIN_FUSED_SEQ_LEN", msl)
     monkeypatch.setattr(config, "REPLACE_CACHE", False)
-    return vb.FusedInt4AttentionImpl(H, D, D ** -0.5, HKV)
+    return vb.FusedInt4AttentionImpl(H, D, scale, HKV)
 
 
 def run_two_steps(vb, impl, dtype, prompt_lens, seed):
@@ -183,7 +181,7 @@ def test_bf16_model_decode(vb, monkeypatch):
                              round_output=False)
     got = r["out_dec"].float().numpy().reshape(ref.shape)
     # bf16 output: half a bf16 ulp (relative 2^-8) on top of the fp32 bar
-    assert close(got, ref, rtol=2.0 ** -8)
+    assert close(got, ref, bf16=True)
 
 
 def test_fp16_paged_write_matches_scatter(vb, monkeypatch):
@@ -205,3 +203,27 @@ def test_fp16_paged_write_matches_scatter(vb, monkeypatch):
     vw.view(-1, HKV, D)[slots[keep]] = v[keep]
     torch.cuda.synchronize()
     assert torch.equal(kc, kw) and torch.equal(vc, vw)
+
+
+@pytest.mark.parametrize("layer_scale", [False, True], ids=["reference_scale", "layer_scale"])
+def test_fused_decode_softmax_scale(vb, monkeypatch, layer_scale):
+    """A layer built with a softmax scale other than 1/sqrt(D): the fused
+    decode uses 1/sqrt(D) as the reference's kernels do (F:924; its
+    _fused_decode passes no scale, F:2851-2928), or the layer's scale when
+    KNLP_FUSED_DECODE_LAYER_SCALE asks for it."""
+    monkeypatch.setattr(config, "FUSED_DECODE_LAYER_SCALE", layer_scale)
+    impl = impl_for(vb, monkeypatch, msl=48, scale=0.05)
+    lens = [70, 33]
+    r = run_two_steps(vb, impl, torch.float16, lens, seed=400)
+    c = impl.caches
+    kp = plane("int4_asym", c.int4_key, c.k_scales, c.k_zeros, config.GROUP_SIZE)
+    vp = plane("int4_asym", c.int4_value, c.v_scales, c.v_zeros, config.GROUP_SIZE)
+    q2 = r["q2"].float().numpy()
+    sl = [n + 1 for n in lens]
+    want = A.decode_reference(q2, kp, vp, r["bt"], sl, scale=0.05 if layer_scale else None,
+                              round_output=False)
+    other = A.decode_reference(q2, kp, vp, r["bt"], sl, scale=None if layer_scale else 0.05,
+                               round_output=False)
+    got = r["out_dec"].float().numpy().reshape(want.shape)
+    assert close(got, want)
+    assert np.abs(got - other).max() > 2e-2      # the two scales give different outputs

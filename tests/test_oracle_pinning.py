@@ -228,3 +228,189 @@ def test_symmetric_dequant_closed_form():
     sc = np.array([[0.5]], np.float16)
     deq = A.dequant_int4(packed, sc, None, 32)
     np.testing.assert_array_equal(deq[0], (codes[0].astype(np.float32) - 8) * 0.5)
+
+
+# ---------------------------------------------------------------------------
+# Dequantisation pinned from explicit floats.  The caches below are built by
+# hand from integer codes and power-of-two scales / quarter-step zeros, so
+# every dequantised value is an exact binary fraction that plain Python
+# arithmetic computes without rounding; the bytes are packed by an explicit
+# per-byte loop (low nibble = element 2i, F:169-170).  The expected values
+# and the textbook softmax never go through the oracle's own dequant code.
+# References: F:164-193 (asymmetric q*scale + zero, symmetric (q-8)*scale),
+# F:1397-1423 (INT8 K: int8 * per-group scale).
+# ---------------------------------------------------------------------------
+
+def _hand_int4(rng, rows, d, gs, asym):
+    """(packed uint8 [rows, d/2], scales fp16 [rows, ng], zeros fp16 or None,
+    expected python floats [rows][d])."""
+    ng = d // gs
+    codes = [[int(rng.integers(0, 16)) for _ in range(d)] for _ in range(rows)]
+    # distinct power-of-two scale per group and quarter-step zero-points, so a
+    # scale or zero read from the wrong group changes the value
+    sc = [[2.0 ** -int(rng.integers(1, 7)) for _ in range(ng)] for _ in range(rows)]
+    zp = [[0.25 * int(rng.integers(-12, 12)) for _ in range(ng)] for _ in range(rows)]
+    packed = np.zeros((rows, d // 2), np.uint8)
+    for r in range(rows):
+        for i in range(d // 2):
+            packed[r, i] = codes[r][2 * i] | (codes[r][2 * i + 1] << 4)
+    want = []
+    for r in range(rows):
+        row = []
+        for e in range(d):
+            g = e // gs
+            if asym:
+                row.append(codes[r][e] * sc[r][g] + zp[r][g])
+            else:
+                row.append((codes[r][e] - 8) * sc[r][g])
+        want.append(row)
+    scales = np.array(sc, np.float16)
+    zeros = np.array(zp, np.float16) if asym else None
+    return packed, scales, zeros, want
+
+
+def _hand_int8(rng, rows, d, gs):
+    ng = d // gs
+    codes = [[int(rng.integers(-128, 128)) for _ in range(d)] for _ in range(rows)]
+    sc = [[2.0 ** -int(rng.integers(3, 12)) for _ in range(ng)] for _ in range(rows)]
+    want = [[codes[r][e] * sc[r][e // gs] for e in range(d)] for r in range(rows)]
+    return np.array(codes, np.int8), np.array(sc, np.float16), want
+
+
+def _int4_pin_holds(dequant, gs=32, d=128, rows=24) -> bool:
+    rng = np.random.default_rng(4242)
+    for asym in (True, False):
+        packed, scales, zeros, want = _hand_int4(rng, rows, d, gs, asym)
+        got = dequant(packed, scales, zeros, gs)
+        if got.shape != (rows, d) or got.tolist() != want:
+            return False
+    return True
+
+
+def _int8_pin_holds(dequant, gs=32, d=128, rows=24) -> bool:
+    rng = np.random.default_rng(4343)
+    for g in (gs, d):
+        codes, scales, want = _hand_int8(rng, rows, d, g)
+        got = dequant(codes, scales, g)
+        if got.shape != (rows, d) or got.tolist() != want:
+            return False
+    return True
+
+
+@pytest.mark.parametrize("gs,d", [(32, 128), (64, 128), (16, 64), (128, 128)])
+def test_dequant_int4_from_explicit_floats(gs, d):
+    assert _int4_pin_holds(A.dequant_int4, gs, d)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_dequant_int8_from_explicit_floats(gs):
+    assert _int8_pin_holds(A.dequant_int8, gs)
+
+
+def test_dequant_pins_reject_planted_mistakes():
+    """The two pins above fail for plausible mistakes planted in a copy of
+    the oracle's dequantisers (on the CPU): the symmetric -8 offset applied
+    in asymmetric mode, the zero added before scaling, a per-element scale
+    index, swapped nibble order, and INT8 codes read as unsigned."""
+    def asym_minus8(packed, scales, zeros, gs):
+        n = Q.unpack_nibbles(packed).astype(np.float32) - 8.0     # offset in both modes
+        g = n.reshape(n.shape[0], -1, gs) * scales.astype(np.float32)[..., None]
+        if zeros is not None:
+            g = g + zeros.astype(np.float32)[..., None]
+        return g.reshape(n.shape)
+
+    def zero_before_scale(packed, scales, zeros, gs):
+        n = Q.unpack_nibbles(packed).astype(np.float32)
+        if zeros is None:
+            return A.dequant_int4(packed, scales, None, gs)
+        g = n.reshape(n.shape[0], -1, gs)
+        return ((g + zeros.astype(np.float32)[..., None])
+                * scales.astype(np.float32)[..., None]).reshape(n.shape)
+
+    def per_element_scale(packed, scales, zeros, gs):
+        n = Q.unpack_nibbles(packed).astype(np.float32)
+        if zeros is None:
+            n = n - 8.0
+        idx = np.arange(n.shape[-1]) % scales.shape[-1]      # element -> scale, wrong
+        out = n * scales.astype(np.float32)[:, idx]
+        if zeros is not None:
+            out = out + zeros.astype(np.float32)[:, idx]
+        return out
+
+    def swapped_nibbles(packed, scales, zeros, gs):
+        sw = ((packed >> 4) | (packed << 4)).astype(np.uint8)
+        return A.dequant_int4(sw, scales, zeros, gs)
+
+    def int8_unsigned(codes, scales, gs):
+        c = np.asarray(codes).view(np.uint8).astype(np.float32)
+        g = c.reshape(c.shape[0], -1, gs) * scales.astype(np.float32)[..., None]
+        return g.reshape(c.shape)
+
+    def int8_group_off_by_one(codes, scales, gs):
+        c = np.asarray(codes, np.int8).astype(np.float32)
+        ng = scales.shape[-1]
+        idx = np.minimum(np.arange(c.shape[-1]) // gs + 1, ng - 1)
+        return c * scales.astype(np.float32)[:, idx]
+
+    assert _int4_pin_holds(A.dequant_int4) and _int8_pin_holds(A.dequant_int8)
+    for bad in (asym_minus8, zero_before_scale, per_element_scale, swapped_nibbles):
+        assert not _int4_pin_holds(bad), bad.__name__
+    for bad in (int8_unsigned, int8_group_off_by_one):
+        assert not _int8_pin_holds(bad), bad.__name__
+
+
+def _textbook_decode(q, rows_k, rows_v, hkv, hq, scale):
+    """softmax(q k / sqrt(D)) v in float64 from python-float rows
+    [T][Hkv][D]; one (sequence) at a time."""
+    import math
+    rep = hq // hkv
+    out = []
+    for h in range(hq):
+        kv = h // rep
+        sc = [scale * sum(float(q[h][e]) * rows_k[t][kv][e] for e in range(len(q[h])))
+              for t in range(len(rows_k))]
+        m = max(sc)
+        w = [math.exp(s - m) for s in sc]
+        tot = sum(w)
+        out.append([sum(w[t] * rows_v[t][kv][e] for t in range(len(rows_v))) / tot
+                    for e in range(len(q[h]))])
+    return np.array(out)
+
+
+@pytest.mark.parametrize("kfmt,vfmt", [("int4_asym", "int4_asym"), ("int4_sym", "int4_sym"),
+                                       ("int8", "int4_asym"), ("int8", "int8")])
+def test_decode_reference_from_explicit_floats(kfmt, vfmt):
+    """decode_reference over hand-built paged caches equals a float64
+    textbook softmax over the explicit floats (gathered through the block
+    table by hand), to fp32 accumulation error."""
+    rng = np.random.default_rng(77)
+    nb, bs, hkv, hq, d, gs = 6, 4, 2, 4, 64, 32
+    planes, rows = {}, {}
+    for side, fmt in (("k", kfmt), ("v", vfmt)):
+        if fmt == "int8":
+            codes, sc, want = _hand_int8(rng, nb * bs * hkv, d, gs)
+            planes[side] = {"format": "int8", "data": codes.reshape(nb, bs, hkv, d),
+                            "scales": sc.reshape(nb, bs, hkv, -1), "zeros": None,
+                            "group_size": gs}
+        else:
+            asym = fmt == "int4_asym"
+            packed, sc, zp, want = _hand_int4(rng, nb * bs * hkv, d, gs, asym)
+            planes[side] = {"format": fmt, "data": packed.reshape(nb, bs, hkv, d // 2),
+                            "scales": sc.reshape(nb, bs, hkv, -1),
+                            "zeros": None if zp is None else zp.reshape(nb, bs, hkv, -1),
+                            "group_size": gs}
+        # python rows indexed [block][offset][head] -> [D] floats
+        rows[side] = [[[want[(b * bs + o) * hkv + h] for h in range(hkv)] for o in range(bs)]
+                      for b in range(nb)]
+    bt = np.array([[4, 1, 5], [2, 0, 3]], np.int32)
+    sl = [11, 6]
+    q = rng.standard_normal((2, hq, d)).astype(np.float16).astype(np.float32)
+    got = A.decode_reference(q, planes["k"], planes["v"], bt, sl, round_output=False)
+    got64 = A.decode_reference_f64(q, planes["k"], planes["v"], bt, sl)
+    scale = float(np.float32(1.0 / np.sqrt(d)))
+    for s in range(2):
+        tk = [rows["k"][bt[s][t // bs]][t % bs] for t in range(sl[s])]
+        tv = [rows["v"][bt[s][t // bs]][t % bs] for t in range(sl[s])]
+        want = _textbook_decode(q[s], tk, tv, hkv, hq, scale)
+        np.testing.assert_allclose(got[s], want, atol=2e-5, rtol=2e-5)
+        np.testing.assert_allclose(got64[s], want, atol=1e-12, rtol=1e-12)
