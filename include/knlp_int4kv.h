@@ -241,6 +241,31 @@ int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads,
                                int32_t k_group_size, int32_t v_format,
                                int32_t v_group_size, int32_t q_dtype);
 
+/*
+ * knlp_kv_decode without a workspace argument and without any allocation:
+ * the split partials go to a 16 MiB array of device memory that the library
+ * holds on each GPU it runs on, from its load until the process ends.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The caller passes inputs and output as for knlp_kv_decode.
+ * A shape whose partials need more than 16 MiB
+ * (num_seqs * num_q_heads * ceil(max_context / split_tokens) * (head_size +
+ * 2) * 4 bytes) returns KNLP_ERR_WORKSPACE.  All calls on one GPU share that
+ * GPU's array: calls that overlap on one GPU (two streams, two threads) race
+ * and must be serialised by the caller.  Nothing in the array needs to start
+ * at zero (every partial the merge reads is written first).
+ */
+int knlp_kv_decode_noalloc(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                           int64_t q_stride_head, int32_t num_seqs, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_size,
+                           const knlp_kv_plane* key_cache,
+                           const knlp_kv_plane* value_cache,
+                           const int32_t* block_table, int64_t bt_stride_seq,
+                           const int32_t* seq_lens, int32_t block_size,
+                           int32_t max_context, float softmax_scale,
+                           int32_t split_tokens, void* out, int32_t out_dtype,
+                           int64_t o_stride_seq, int64_t o_stride_head, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

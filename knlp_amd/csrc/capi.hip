@@ -1,6 +1,7 @@
 // extern "C" entry points: argument validation, split planning, dispatch.
 // No allocation and no synchronisation happens here; every launch goes to
 // the caller's stream.
+#include <atomic>
 #include <cmath>
 
 #include "kv_decode.h"
@@ -441,3 +442,63 @@ int knlp_int4_twos_to_offset(const void* src, int64_t src_stride_row, void* dst,
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Decode with no allocation at all: the split partials live in a file-scope
+// device array that each GPU holds from the library's load until the process
+// ends.  In host code `scratch` names a host-side stand-in, never the device
+// array: host code uses only the per-device address from
+// hipGetSymbolAddress below.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kScratchBytes = 16LL << 20;   // 16 MiB per GPU
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+
+// This device's copy of `scratch`, looked up once per device (with that
+// device current, as hipGetDevice reports it); nullptr on failure.
+void* device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  void* q = nullptr;
+  if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || q == nullptr) return nullptr;
+  g_scratch[dev].store(q, std::memory_order_release);   // a racing store writes the same value
+  return q;
+}
+
+}  // namespace
+
+extern "C" int knlp_kv_decode_noalloc(const void* query, int32_t q_dtype, int64_t q_stride_seq,
+                                      int64_t q_stride_head, int32_t num_seqs,
+                                      int32_t num_q_heads, int32_t num_kv_heads,
+                                      int32_t head_size, const knlp_kv_plane* key_cache,
+                                      const knlp_kv_plane* value_cache,
+                                      const int32_t* block_table, int64_t bt_stride_seq,
+                                      const int32_t* seq_lens, int32_t block_size,
+                                      int32_t max_context, float softmax_scale,
+                                      int32_t split_tokens, void* out, int32_t out_dtype,
+                                      int64_t o_stride_seq, int64_t o_stride_head,
+                                      void* stream) {
+  if (num_seqs < 0 || num_q_heads <= 0 || head_size <= 0 || max_context <= 0 ||
+      split_tokens <= 0)
+    return KNLP_ERR_SHAPE;
+  if (num_seqs == 0) return KNLP_OK;
+  const int64_t ns = (static_cast<int64_t>(max_context) + split_tokens - 1) / split_tokens;
+  if (ns > 65535) return KNLP_ERR_SHAPE;
+  // every partial the merge reads is written by the partial kernel first, so
+  // nothing in the scratch has to start at zero
+  const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, static_cast<int>(ns)) * 4;
+  if (need > kScratchBytes) return KNLP_ERR_WORKSPACE;
+  void* ws = device_scratch();
+  if (ws == nullptr) return KNLP_ERR_LAUNCH;
+  return knlp_kv_decode(query, q_dtype, q_stride_seq, q_stride_head, num_seqs, num_q_heads,
+                        num_kv_heads, head_size, key_cache, value_cache, block_table,
+                        bt_stride_seq, seq_lens, block_size, max_context, softmax_scale,
+                        split_tokens, ws, kScratchBytes, out, out_dtype, o_stride_seq,
+                        o_stride_head, stream);
+}
