@@ -31,11 +31,20 @@
 //     scale placement of docs/fused-quant/fp8-attention-hardware-notes.md:108-113.
 // PV  The V scale depends on the token, which is the contraction index, so
 //     it goes into the probabilities: P'[(g,vg), t] = p[g,t] * s_v[t,vg], split
-//     into fp16 hi + lo (about 22 significant bits).  B = the V codes; the
-//     zero-point (asymmetric) or -8 s (symmetric) folds into a per-row term
-//     sum_t p * z, accumulated in fp32.  Output rows are (g, vg) pairs and
+//     into fp16 hi + lo.  B = the V codes; the zero-point (asymmetric) or
+//     -8 s (symmetric; -128 s for the biased INT8 codes) folds into a per-row
+//     term sum_t p * z, accumulated in fp32.  Output rows are (g, vg) pairs and
 //     columns are head_dim elements; a column's value is kept only in the row
 //     whose vg is the column's group.
+//     Precision of P': p carries a per-wave power of two 2^k chosen from the
+//     largest V scale seen so far (k lowered, with the accumulators rescaled,
+//     when a larger one arrives), so that max_t P' lies near 2^12..2^14 however
+//     small the V scales are.  The dominant terms then have a normal fp16 hi
+//     and lo, P' keeps about 22 significant bits, and fp16's absolute floor
+//     (2^-24) sits 2^-36 or more below the largest V scale.  hi is rounded
+//     toward zero by one explicit conversion and lo is the exact product minus
+//     that same hi, so the matrix cores see hi + lo = p * s_v to 2^-22 and the
+//     symmetric bias term (computed from p * s_v in fp32) cancels against it.
 // Both operands of PV need "lane = row/column, registers = tokens", but
 // they arrive as "lane = token".  P' is transposed on the matrix cores
 // (v_mfma_f32_16x16x16_f16 against the identity).  V is transposed either
@@ -47,8 +56,8 @@
 // D[4*(l/16) + i][l % 16] in register i.
 //
 // Online softmax: a row's running max is raised only when a tile's max
-// exceeds it by more than 2 (log2 units).  Then p <= 4 and |P'| <= 4 * s_v,
-// which stays inside fp16 range for any finite fp16 K/V input (s_v < 9400).
+// exceeds it by more than 2 (log2 units).  Then p <= 4 * 2^k and
+// |P'| <= 4 * 2^k * s_v <= 2^14, inside fp16 range for any finite input.
 
 #include <type_traits>
 
@@ -301,6 +310,7 @@ __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane,
 template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH, int NGK = NG, bool V8 = false>
 struct WaveState {
   static constexpr int GPL = 4 / NG;
+  static constexpr int NGV = NG;       // V scale groups per token
   // V codes: packed INT4 (one dword of 8 nibble-columns per token and lane in
   // pv_columns) or INT8 (V8: 8 bytes)
   using VWord = typename std::conditional<V8, uint2, uint32_t>::type;
@@ -325,6 +335,8 @@ struct WaveState {
   float zacc[4];       // per-lane zero-point term, rows 4blk + e
   float sl2[GPL];      // softmax_scale * log2(e) * 2^24 / (the row's q scale)
   float thr[GPL];      // rescale threshold 2 / sl2 (score units)
+  float kexp;          // k: p, lsum, zacc and acc carry the factor 2^k (wave-uniform)
+  float svlim;         // 2^(12 - k): a V scale above it takes the slow path
 
   // Scores of the two sub-tiles in units of 2^-24:
   //   sum_kg s[t,kg] * S[(g,kg),t] + z[t,kg] * qsum24[(g,kg)].
@@ -360,30 +372,69 @@ struct WaveState {
     }
   }
 
-  // Does any row's tile max exceed its running max by more than thr?  No
-  // cross-lane reduction: a lane-wise test and a ballot.
-  __device__ __forceinline__ bool max_moves(const float (&score)[2][GPL]) const {
-    bool up = false;
+  // V scales of the two sub-tiles as fp32; tokens past the end read 0 (their
+  // bytes are stale).
+  template <bool MASK>
+  __device__ __forceinline__ void vscales(const ST (&st)[2], const bool (&valid)[2],
+                                          float (&sv)[2][NG]) const {
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        sv[x][g] = st[x].vs.get(g);
+        if constexpr (MASK) sv[x][g] = valid[x] ? sv[x][g] : 0.0f;
+      }
+  }
+
+  __device__ __forceinline__ static float max_sv(const float (&sv)[2][NG]) {
+    float m = sv[0][0];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) m = fmaxf(m, sv[x][g]);
+    return m;
+  }
+
+  // Does any row's tile max exceed its running max by more than thr, or any
+  // V scale exceed svlim?  No cross-lane reduction: lane-wise tests and one
+  // ballot.
+  __device__ __forceinline__ bool slow_tile(const float (&score)[2][GPL],
+                                            const float (&sv)[2][NG]) const {
+    bool up = max_sv(sv) > svlim;
 #pragma unroll
     for (int gi = 0; gi < GPL; ++gi) up |= fmaxf(score[0][gi], score[1][gi]) > m_run[gi] + thr[gi];
     return __any(up);
   }
 
   // Raise the running max of the rows whose tile max exceeds it by more than
-  // thr, and rescale their accumulators.
-  __device__ __forceinline__ void raise_max(const float (&score)[2][GPL]) {
+  // thr, lower k when a V scale of the tile exceeds svlim, and rescale the
+  // accumulators by both factors (powers of two for k, so exact).
+  __device__ __forceinline__ void slow_step(const float (&score)[2][GPL],
+                                            const float (&sv)[2][NG]) {
+    // k from the largest V scale of the tile over the wave: s <= 2^e, and
+    // 2^k * s <= 2^12.  k only decreases (it starts at 40, far above any
+    // fp16 scale's need: fp16 scales are at least 2^-24).
+    float smax = row_max16(max_sv(sv));
+    smax = fmaxf(smax, __shfl_xor(smax, 16, kWave));
+    smax = fmaxf(smax, __shfl_xor(smax, 32, kWave));
+    int e = 0;
+    frexpf(smax, &e);                                // smax = 0 gives e = 0
+    const float knew = fminf(kexp, static_cast<float>(12 - e));
+    const float kscale = ldexpf(1.0f, static_cast<int>(knew - kexp));   // 2^(knew - k) <= 1
+    kexp = knew;
+    svlim = ldexpf(1.0f, 12 - static_cast<int>(knew));
     float alpha[GPL];
 #pragma unroll
     for (int gi = 0; gi < GPL; ++gi) {
       const float tmax = row_max16(fmaxf(score[0][gi], score[1][gi]));
       const bool up = tmax > m_run[gi] + thr[gi];
-      alpha[gi] = up ? __builtin_amdgcn_exp2f((m_run[gi] - tmax) * sl2[gi]) : 1.0f;
+      alpha[gi] = (up ? __builtin_amdgcn_exp2f((m_run[gi] - tmax) * sl2[gi]) : 1.0f) * kscale;
       m_run[gi] = up ? tmax : m_run[gi];
     }
 #pragma unroll
     for (int gi = 0; gi < GPL; ++gi) lsum[gi] *= alpha[gi];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) zacc[e] *= alpha[e / NG];
+    for (int e4 = 0; e4 < 4; ++e4) zacc[e4] *= alpha[e4 / NG];
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
@@ -392,26 +443,26 @@ struct WaveState {
         for (int i = 0; i < 4; ++i) acc[c][h][i] *= alpha[i / NG];
   }
 
-  // Probabilities p, P' = p * s_v split into fp16 hi + lo and transposed to
-  // the PV A operand (lane = row (g, vg), slots = tokens), and the
-  // zero-point term, for the two sub-tiles.
+  // Probabilities p (times 2^k), P' = p * s_v split into fp16 hi + lo and
+  // transposed to the PV A operand (lane = row (g, vg), slots = tokens), and
+  // the zero-point term, for the two sub-tiles.
   template <bool MASK>
   __device__ __forceinline__ void probs(const ST (&st)[2], const bool (&valid)[2],
-                                        const float (&score)[2][GPL], h8& ahi, h8& alo) {
+                                        const float (&score)[2][GPL], const float (&svt)[2][NG],
+                                        h8& ahi, h8& alo) {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       float p[GPL];
 #pragma unroll
       for (int gi = 0; gi < GPL; ++gi) {
-        // (score - max) first: the token that sets the max gets p = 1 exactly
-        p[gi] = __builtin_amdgcn_exp2f((score[x][gi] - m_run[gi]) * sl2[gi]);   // 0 when masked
-        lsum[gi] += p[gi];
+        // (score - max) first: the token that sets the max gets p = 2^k exactly
+        p[gi] = __builtin_amdgcn_exp2f(fmaf(score[x][gi] - m_run[gi], sl2[gi], kexp));
+        lsum[gi] += p[gi];                                    // 0 when masked
       }
       float sv[4], P[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        sv[e] = st[x].vs.get(e % NG);
-        if constexpr (MASK) sv[e] = valid[x] ? sv[e] : 0.0f;   // garbage past the end
+        sv[e] = svt[x][e % NG];
         P[e] = p[e / NG] * sv[e];
         if constexpr (VASYM) {
           float zv = st[x].vz.get(e % NG);
@@ -422,14 +473,16 @@ struct WaveState {
           zacc[e] = fmaf(V8 ? -128.0f : -8.0f, P[e], zacc[e]);
         }
       }
-      const h2 hi01 = {static_cast<_Float16>(P[0]), static_cast<_Float16>(P[1])};
-      const h2 hi23 = {static_cast<_Float16>(P[2]), static_cast<_Float16>(P[3])};
+      // hi by one explicit conversion (toward zero), lo = p * s_v - hi exactly
+      // rounded: both halves derive from the same hi bits
+      const h2 hi01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(P[0], P[1]));
+      const h2 hi23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(P[2], P[3]));
       const float r0 = fmaf(p[0 / NG], sv[0], -static_cast<float>(hi01[0]));
       const float r1 = fmaf(p[1 / NG], sv[1], -static_cast<float>(hi01[1]));
       const float r2 = fmaf(p[2 / NG], sv[2], -static_cast<float>(hi23[0]));
       const float r3 = fmaf(p[3 / NG], sv[3], -static_cast<float>(hi23[1]));
-      const h2 lo01 = {static_cast<_Float16>(r0), static_cast<_Float16>(r1)};
-      const h2 lo23 = {static_cast<_Float16>(r2), static_cast<_Float16>(r3)};
+      const h2 lo01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+      const h2 lo23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(r2, r3));
       const h4 xhi = {hi01[0], hi01[1], hi23[0], hi23[1]};
       const h4 xlo = {lo01[0], lo01[1], lo23[0], lo23[1]};
       const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
@@ -556,15 +609,6 @@ struct WaveState {
     }
   }
 
-  template <bool MASK>
-  __device__ __forceinline__ void accumulate(const ST (&st)[2],
-                                             const bool (&valid)[2],
-                                             const float (&score)[2][GPL]) {
-    h8 ahi, alo;
-    probs<MASK>(st, valid, score, ahi, alo);
-    pv_transposed(st, ahi, alo);
-  }
-
   // General step: any tile, masked or not, max moving or not.
   template <bool MASK>
   __device__ __forceinline__ void step(const ST (&st)[2], int tbase, int t_end,
@@ -576,8 +620,12 @@ struct WaveState {
     }
     float score[2][GPL];
     scores<MASK>(st, valid, score);
-    if (max_moves(score)) raise_max(score);
-    accumulate<MASK>(st, valid, score);
+    float sv[2][NG];
+    vscales<MASK>(st, valid, sv);
+    if (slow_tile(score, sv)) slow_step(score, sv);
+    h8 ahi, alo;
+    probs<MASK>(st, valid, score, sv, ahi, alo);
+    pv_transposed(st, ahi, alo);
   }
 
 };
@@ -677,6 +725,9 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.zacc[e] = 0.0f;
+  // no V scale seen yet: the first tile sets k (every fp16 scale exceeds 2^-28)
+  W.kexp = 40.0f;
+  W.svlim = 0x1p-28f;
   // scores are in units of 2^-24 times the row's q scale
 #pragma unroll
   for (int gi = 0; gi < GPL; ++gi) {
@@ -698,8 +749,10 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
   constexpr int GPL = 4 / NG;
   const int G = min(heads_per_set<NG>(), a.group - hs);   // heads of this set
   const int gs = a.vp.group_size;
+  // acc, zacc and lsum carry 2^k
+  const float kinv = ldexpf(1.0f, -static_cast<int>(W.kexp));
 #pragma unroll
-  for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]);
+  for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]) * kinv;
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.zacc[e] = row_sum16(W.zacc[e]);
   const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * a.group + hs;
@@ -717,7 +770,7 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
           const int64_t row = (row0 + g) * a.num_splits + split;
           // pv_columns' odd INT4 columns carry a factor 16
           a.part_o[row * D + d] =
-              fmaf(W.acc[c][h][i], COLS && h && !V8 ? 0x1p20f : 0x1p24f, W.zacc[i]);
+              fmaf(W.acc[c][h][i], COLS && h && !V8 ? 0x1p20f : 0x1p24f, W.zacc[i]) * kinv;
         }
       }
     }
@@ -1095,10 +1148,12 @@ __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int 
   }
   // tile i's V replaces tile i - 1's in place once its PV has consumed it
   coop_read_v<L, D>(cur, wave, col, blk, vw);
+  float sv[2][WS::NGV];
+  W[0].template vscales<MASK>(st, valid, sv);
 #pragma unroll
   for (int s = 0; s < NSET; ++s) {
-    if (W[s].max_moves(score[s])) W[s].raise_max(score[s]);
-    W[s].template probs<MASK>(st, valid, score[s], ahi[s], alo[s]);
+    if (W[s].slow_tile(score[s], sv)) W[s].slow_step(score[s], sv);
+    W[s].template probs<MASK>(st, valid, score[s], sv, ahi[s], alo[s]);
   }
   // copies issued after tile i + 1's: tiles i + 2 .. min(i + NBUF - 1, ntiles - 1)
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);

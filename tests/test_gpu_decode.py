@@ -25,13 +25,15 @@ ATOL = tolerance.ATOL
 
 
 def _build(seq_lens, hq, hkv, d, kfmt, vfmt, kgs, vgs, seed, bs=16, pool=None,
-           outliers=0.01, clip=10.0):
+           outliers=0.01, clip=10.0, vsigma=1.0):
     nb = pool or max(sum(-(-int(n) // bs) for n in seq_lens), 1) + 3
     bt = kvgen.paged_table(seq_lens, bs, nb, 6000 + seed)
     slots = kvgen.token_slots(bt, seq_lens, bs)
     nt = len(slots)
     k = kvgen.randn((nt, hkv, d), 2000 + seed, torch.float16, outliers).float().numpy()
     v = kvgen.randn((nt, hkv, d), 3000 + seed, torch.float16, outliers).float().numpy()
+    if vsigma != 1.0:
+        v = (v * vsigma).astype(np.float16).astype(np.float32)
     kp = kvgen.empty_plane(kfmt, nb, bs, hkv, d, kgs)
     vp = kvgen.empty_plane(vfmt, nb, bs, hkv, d, vgs)
     if nt:
@@ -70,8 +72,14 @@ def _run(query, kp, vp, bt, seq_lens, hkv, d, split_tokens=None):
     elif kf == "fp16" and vf == "int8":
         out = K.kfp16_vint8_decode(q, kd, vd, vs, btd, sl, hkv, d,
                                    v_group_size=vp["group_size"], **kw)
-    else:
+    elif kf == "fp16" and vf == "fp16":
         out = K.fp16_paged_decode(q, kd, vd, btd, sl, hkv, d, **kw)
+    else:                     # pairs without a reference-named function (INT4 K, INT8 V)
+        from knlp_amd import ops
+        fmt = {"int4_sym": 0, "int4_asym": 1, "int8": 2, "fp16": 3}
+        out = ops._decode(q, ops._plane(kd, ks, kz, fmt[kf], kp["group_size"]),
+                          ops._plane(vd, vs, vz, fmt[vf], vp["group_size"]), kd.shape[1], btd,
+                          sl, hkv, d, **kw)
     torch.cuda.synchronize()
     return out
 
@@ -327,3 +335,37 @@ def test_mixed_int4_formats_through_the_abi(kfmt, vfmt, hkv, hq):
                       torch.tensor(seq_lens, dtype=torch.int32, device=DEV), hkv, 128)
     torch.cuda.synchronize()
     _check(out, q, kp, vp, bt, seq_lens)
+
+
+SMALL_V_CASES = [
+    # name, seq_lens, hq, hkv, kfmt, vfmt, kgs, vgs
+    ("coop_kint8_vint8_row", [640, 17], 32, 8, 2, 2, 128, 128),
+    ("coop_kint8_vint8_g32", [700, 33], 32, 8, 2, 2, 128, 32),
+    ("coop_kint4_vint8_g32", [500, 1], 32, 8, 1, 2, 32, 32),
+    ("coop_int4_asym", [900, 40], 32, 8, 1, 1, 32, 32),
+    ("coop_int4_sym", [900, 40], 32, 8, 0, 0, 32, 32),
+    ("coop_kint8_row_vint4_g5", [700, 3], 40, 8, 2, 1, 128, 32),
+    ("perhead_int4_asym_hkv4", [800, 65], 16, 4, 1, 1, 32, 32),
+    ("perhead_int4_sym_hkv4", [800, 65], 16, 4, 0, 0, 32, 32),
+    ("perhead_kfp16_vint8_hkv4", [600, 17], 16, 4, 3, 2, 128, 32),
+    ("perhead_kfp16_vint8_row", [600, 17], 32, 8, 3, 2, 128, 128),
+]
+
+
+@pytest.mark.parametrize("sigma", [1e-2, 1e-3, 1e-4])
+@pytest.mark.parametrize("case", SMALL_V_CASES, ids=[c[0] for c in SMALL_V_CASES])
+def test_small_magnitude_v_keeps_relative_accuracy(case, sigma):
+    """V of small magnitude (N(0, sigma^2), sigma down to 1e-4, so V scales
+    down to ~1e-6): the output must keep the accuracy it has at sigma = 1,
+    relative to its own scale.  Checked as out / sigma against oracle / sigma
+    with the usual bar (the decode is linear in V).  Before P' carried a
+    power-of-two factor, fp16's absolute floor in the P' = p * s_v split cost
+    up to 12 % of the output at sigma = 1e-3 with INT8 V."""
+    name, seq_lens, hq, hkv, kf, vf, kgs, vgs = case
+    d = 128
+    seed = zlib.crc32(name.encode()) % 1000
+    bt, kp, vp = _build(seq_lens, hq, hkv, d, kf, vf, kgs, vgs, seed, vsigma=sigma)
+    q = _query(len(seq_lens), hq, d, seed)
+    out = _run(q, kp, vp, bt, seq_lens, hkv, d)
+    ref = A.decode_reference(q.float().numpy(), kp, vp, bt, seq_lens, round_output=False)
+    tolerance.check(f"small_v[{name}-{sigma:g}]", out.float().cpu().numpy() / sigma, ref / sigma)

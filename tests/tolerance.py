@@ -19,7 +19,9 @@ F16_KNEE = 2.0
 RTOL_F16 = 2.0 ** -10
 RTOL_BF16 = 2.0 ** -8
 
-RESULTS: list[tuple[str, float, float]] = []   # (case, max-abs error, max |ref|)
+# (case, max-abs error where |ref| <= 2, max error / bar over all elements,
+#  max-abs error over all elements, max |ref|)
+RESULTS: list[tuple[str, float, float, float, float]] = []
 
 
 def bound(ref: np.ndarray, bf16: bool = False) -> np.ndarray:
@@ -37,8 +39,12 @@ def check(name: str, got: np.ndarray, ref: np.ndarray, bf16: bool = False) -> fl
     assert np.isfinite(got).all(), f"{name}: non-finite output"
     err = np.abs(got - ref)
     m = float(err.max()) if err.size else 0.0
-    RESULTS.append((name, m, float(np.abs(ref).max()) if ref.size else 0.0))
-    over = err > bound(ref, bf16)
+    b = bound(ref, bf16)
+    small = np.abs(ref) <= F16_KNEE
+    RESULTS.append((name, float(err[small].max()) if small.any() else 0.0,
+                    float((err / b).max()) if err.size else 0.0, m,
+                    float(np.abs(ref).max()) if ref.size else 0.0))
+    over = err > b
     assert not over.any(), (f"{name}: max abs err {m:.3e}; {int(over.sum())} elements over "
                             f"the bar, worst at |ref| = {float(np.abs(ref)[over].max()):.3g}")
     return m
