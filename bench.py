@@ -25,9 +25,21 @@
   inputs before timing; ``config.split_tokens_planned`` and
   ``config.split_sweep_us_per_step`` record the choice (``--no-split-sweep``
   times the plan alone).  The fp16 leg picks its split the same way.
+* ``stream_ceiling`` is a plain read of the partial kernel's byte count by
+  the library's read probe, the best of a few launch shapes: the sustained
+  HBM read rate of this GPU, beside the data-sheet 8 TB/s.
+* ``roofline.traffic`` is the counter-measured HBM bytes per launch from
+  ``profiles/decode_cfgC_traffic.json`` when those were measured on the
+  kernel sources as they are (a hash of the sources is stored with them),
+  else null with the reason.
 * ``cpu_baseline`` times the oracle's dequantise -> repeat_interleave -> SDPA
-  path (the reference's P1 pipeline) in torch on the host cores.  It runs on
-  a bounded sample (one sequence) and is scaled to the whole step.
+  path (the reference's P1 pipeline) in torch fp32 on all the host CPUs this
+  process may use: the whole step when one step takes at most ~2.5 s of CPU
+  time, otherwise the first sequences that fit, reported as that sample's
+  GB/s (no per-step time is extrapolated).  Its outputs are the parity check
+  of those sequences.
+* ``--config 6`` is the reference's default serving mode, symmetric INT4
+  with the trimmed-mean clip (F:70-77, F:328-357), at config 2's shape.
 """
 from __future__ import annotations
 
@@ -60,8 +72,89 @@ CONFIGS = {
     5: dict(name="qwen-gqa5 B16 T65536 K-int8-row V-int4-asym-g32 +append", B=16, Hq=40,
             Hkv=8, D=128, T=65536, kfmt="int8", vfmt="int4_asym", kgs=128, vgs=32,
             paged=False, outliers=0.0, append=True),
+    # the reference's default serving mode (ASYMMETRIC=0, OUTLIER_CLIP_RATIO=10,
+    # F:70-77; quantiser F:328-357) at config 2's shape
+    6: dict(name="llama3-8b-gqa B8 T32768 int4-sym-g32-clip10 outliers1%x20", B=8, Hq=32,
+            Hkv=8, D=128, T=32768, kfmt="int4_sym", vfmt="int4_sym", kgs=32, vgs=32,
+            paged=False, outliers=0.01, append=False, clip=10.0),
 }
 FMT = {"int4_sym": 0, "int4_asym": 1, "int8": 2, "fp16": 3}
+
+
+DTYPES = {
+    1: "int4-asym-g32 KV, fp16 q, fp32 accumulate",
+    2: "int4-asym-g32 KV, fp16 q, fp32 accumulate",
+    3: "int4-asym-g32 KV, fp16 q, fp32 accumulate",
+    4: "int4-asym-g64 KV, fp16 q, fp32 accumulate",
+    5: "int8 K / int4-asym V, fp16 q, fp32 accumulate",
+    6: "int4-sym-g32 KV (trimmed-mean clip 10), fp16 q, fp32 accumulate",
+}
+# kernel sources whose code decides the partial kernel's HBM traffic; a
+# committed counter measurement counts only while they are unchanged
+TRAFFIC_SOURCES = ("knlp_amd/csrc/kv_decode_mfma.hip", "knlp_amd/csrc/kv_decode.h",
+                   "knlp_amd/csrc/kv_quant.h", "knlp_amd/csrc/kv_common.h")
+
+
+def kernel_source_hash():
+    import hashlib
+    h = hashlib.sha256()
+    for f in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(c):
+    """HBM bytes per launch of the partial kernel from the committed rocprofv3
+    counter runs (profiles/decode_cfgC_traffic.json), if they were measured on
+    the kernel sources as they are now; else (None, reason)."""
+    tf = os.path.join(ROOT, "profiles", f"decode_cfg{c}_traffic.json")
+    if not os.path.exists(tf):
+        return None, "no counter measurement for this config"
+    try:
+        rec = json.load(open(tf))
+    except (OSError, ValueError):
+        return None, "unreadable counter record"
+    if rec.get("kernel_source_sha256") != kernel_source_hash():
+        return None, (f"stale: {os.path.relpath(tf, ROOT)} was measured on other kernel "
+                      f"sources (hash {rec.get('kernel_source_sha256')}, now "
+                      f"{kernel_source_hash()})")
+    return rec.get("hbm_bytes_per_launch"), (f"{os.path.relpath(tf, ROOT)}: rocprofv3 "
+                                             f"FETCH_SIZE + WRITE_SIZE, same kernel sources")
+
+
+def stream_ceiling(L, nbytes, copies, dev, launches=30):
+    """Time the library's plain read probe over `nbytes` (rotating `copies`
+    buffers so the MALL cannot serve a launch from the previous one), for a
+    few workgroup counts; the fastest is the sustained-read ceiling."""
+    from knlp_amd._lib import check
+    from knlp_amd.ops import _stream
+    n = (nbytes + 15) // 16 * 16
+    bufs = [torch.ones(n // 4, dtype=torch.int32, device=dev) for _ in range(copies)]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.zeros(8 * cus, dtype=torch.int32, device=dev)
+    best = None
+    for blocks in (cus, 2 * cus, 4 * cus, 8 * cus):
+        def go(k):
+            for i in range(k):
+                check(L.knlp_hbm_read_probe(bufs[i % copies].data_ptr(), n, sink.data_ptr(),
+                                            blocks, _stream()), "knlp_hbm_read_probe")
+        go(5)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        go(launches)
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / launches
+        if best is None or us < best[0]:
+            best = (us, blocks)
+    del bufs
+    gbs = n / (best[0] * 1e-6) / 1e9
+    return {"bytes": n, "us": round(best[0], 2), "GBs": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "workgroups": best[1],
+            "kernel": "knlp_hbm_read_probe (16-byte loads, 8 in flight per lane, one "
+                      "contiguous slice per workgroup)"}
 
 
 def per_token_head_bytes(fmt, d, gs):
@@ -153,7 +246,7 @@ class Caches:
         return _plane(self.data, self.scales, self.zeros, FMT[self.fmt], self.gs)
 
 
-def fill(c: Caches, rows, slots, block_size):
+def fill(c: Caches, rows, slots, block_size, clip=0.0):
     import knlp_amd as K
     if c.fmt == "fp16":
         blk, off = slots // block_size, slots % block_size
@@ -162,54 +255,124 @@ def fill(c: Caches, rows, slots, block_size):
         K.reshape_and_cache_k_int8(rows, c.data, c.scales, slots, group_size=c.gs)
     else:
         K.reshape_and_cache_v_only_int4(rows, c.data, c.scales, slots, c.zeros,
-                                        asymmetric=c.fmt == "int4_asym", group_size=c.gs)
+                                        asymmetric=c.fmt == "int4_asym", group_size=c.gs,
+                                        clip_ratio=clip)
 
 
-def time_cpu_baseline(cfg, q_cpu, kc: Caches, vc: Caches, bt, seq_lens, bs):
-    """Oracle dequant -> repeat_interleave -> SDPA on the host, one sequence."""
+def _host_threads():
+    """CPUs this process may run on (the box's share, whatever os.cpu_count()
+    reports for the whole machine)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def _mem_available():
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    return None
+
+
+def time_cpu_baseline(cfg, q_cpu, kc: Caches, vc: Caches, bt, seq_lens, bs, budget_s=20.0):
+    """The reference's CPU path (the oracle's dequantise -> repeat_interleave
+    -> SDPA in torch fp32, scripts/v35_h100_bench.py:376-387) on the host
+    cores, timed per BASELINE's CPU plan: all the CPUs this process may use,
+    median over timed passes after a warm pass.  A pass covers the whole step
+    when one step fits about 2.5 s of CPU time, otherwise the first sequences
+    (longest first for variable lengths) that do; the throughput is that
+    sample's algorithmic bytes over its time, and no per-step time is
+    extrapolated from a partial sample.  Returns (record, {seq: ref}) or
+    (record with "skipped", {})."""
     sys.path.insert(0, ROOT)
     from oracle import attention as A
-    threads = min(os.cpu_count() or 1, 16)
+    threads = _host_threads()
     torch.set_num_threads(threads)
-    s = int(np.argmax(seq_lens)) if cfg["paged"] else 0
-    n = int(seq_lens[s])
-    nblk = -(-n // bs)
-    blocks = torch.from_numpy(bt[s, :nblk].astype(np.int64)).to(kc.data.device)
+    B = cfg["B"]
+    order = [int(i) for i in (np.argsort(-seq_lens, kind="stable") if cfg["paged"] else range(B))]
+    # host RAM for one sequence: fp32 K/V expanded over the q heads (the
+    # reference's repeat_interleave), plus the dequantised planes
+    need = int(seq_lens[order[0]]) * (cfg["Hq"] * 2 + cfg["Hkv"] * 2) * cfg["D"] * 4
+    avail = _mem_available()
+    base = {"unit": "GB/s", "cores": threads, "kind": "port", "os_cpu_count": os.cpu_count(),
+            "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model()}
+    if avail is not None and need > avail // 2:
+        return {**base, "value": None, "skipped": f"RAM: a sequence needs {need >> 20} MiB, "
+                                                   f"{avail >> 20} MiB available"}, {}
 
-    def host_plane(c: Caches):
-        d = {"format": c.fmt, "group_size": c.gs, "data": c.data[blocks].cpu().numpy(),
-             "scales": None if c.scales is None else c.scales[blocks].cpu().numpy(),
-             "zeros": None if c.zeros is None else c.zeros[blocks].cpu().numpy()}
-        return d
+    def host_plane(c: Caches, blocks):
+        return {"format": c.fmt, "group_size": c.gs, "data": c.data[blocks].cpu().numpy(),
+                "scales": None if c.scales is None else c.scales[blocks].cpu().numpy(),
+                "zeros": None if c.zeros is None else c.zeros[blocks].cpu().numpy()}
 
-    kp, vp = host_plane(kc), host_plane(vc)
-    local_bt = np.arange(nblk, dtype=np.int32)[None]
-    q = q_cpu[s:s + 1].float().numpy()
+    inputs = {}
+
+    def prepare(s):
+        n = int(seq_lens[s])
+        nblk = -(-n // bs)
+        blocks = torch.from_numpy(bt[s, :nblk].astype(np.int64)).to(kc.data.device)
+        inputs[s] = (q_cpu[s:s + 1].float().numpy(), host_plane(kc, blocks),
+                     host_plane(vc, blocks), np.arange(nblk, dtype=np.int32)[None], [n])
+
+    def run(sample):
+        return {s: A.decode_reference(*inputs[s])[0] for s in sample}
+
+    prepare(order[0])
+    t0 = time.perf_counter()
+    refs = run(order[:1])
+    t_one = time.perf_counter() - t0
+    sample = [order[0]]
+    for s in order[1:]:
+        if t_one * (len(sample) + 1) > 2.5:
+            break
+        sample.append(s)
+    for s in sample[1:]:
+        prepare(s)
+    run(sample)                                    # warm pass
+    t_pass = max(t_one * len(sample), 1e-6)
+    n_timed = int(max(3, min(10, budget_s // t_pass)))
     times = []
-    out = None
-    for _ in range(3):
+    for _ in range(n_timed):
         t0 = time.perf_counter()
-        out = A.decode_reference(q, kp, vp, local_bt, [n])
+        refs = run(sample)
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
-    sample_bytes = algorithmic_bytes({**cfg, "B": 1}, [n], cfg["kfmt"], cfg["vfmt"], bs)
-    return {"value": round(sample_bytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"sequence {s} ({n} tokens, {cfg['Hq']}q/{cfg['Hkv']}kv heads) of the "
-                      f"workload; median of 3 runs of the oracle's dequant->SDPA in torch fp32",
-            "us_per_seq": round(t * 1e6, 1),
-            "us_per_step_equiv": round(t * 1e6 * float(np.sum(seq_lens)) / n, 1),
-            "cpu_model": _cpu_model()}, out, s
+    lens = [int(seq_lens[s]) for s in sample]
+    sample_bytes = algorithmic_bytes({**cfg, "B": len(sample)}, lens, cfg["kfmt"], cfg["vfmt"], bs)
+    whole = len(sample) == B
+    rec = {**base, "value": round(sample_bytes / t / 1e9, 3),
+           "sample": (f"{'the whole step' if whole else f'{len(sample)} of {B} sequences'} "
+                      f"({sum(lens)} tokens, {cfg['Hq']}q/{cfg['Hkv']}kv heads); median of "
+                      f"{n_timed} timed passes after one warm pass, torch fp32 on {threads} "
+                      f"threads"),
+           "us_per_pass": round(t * 1e6, 1), "timed_passes": n_timed}
+    if whole:
+        rec["us_per_step"] = round(t * 1e6, 1)
+    return rec, refs
 
 
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it (model name, family / model /
+    stepping numbers, sockets)."""
+    fields, sockets = {}, set()
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" not in line:
+                continue
+            k, v = (x.strip() for x in line.split(":", 1))
+            if k == "physical id":
+                sockets.add(v)
+            elif k in ("model name", "cpu family", "model", "stepping") and k not in fields:
+                fields[k] = v
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    return (f"{name} (family {fields.get('cpu family', '?')}, model {fields.get('model', '?')}, "
+            f"stepping {fields.get('stepping', '?')}; {max(len(sockets), 1)} socket(s))")
 
 
 def run_decode_steps(copies, q, bt_d, sl_d, cfg, bs, split, ws, out, steps, partial_only=False,
@@ -303,8 +466,12 @@ def main(argv=None):
     bt, nb = make_block_table(cfg, seq_lens, bs, 6000 + c)
     L = lib()
     max_context = bt.shape[1] * bs
-    split_plan = L.knlp_kv_decode_split_tokens(
-        B, Hkv, Hq, D, max_context, FMT[cfg["kfmt"]], FMT[cfg["vfmt"]])
+    # the library's plan from what a serving loop knows on the host: shapes,
+    # group sizes and the batch's total context (vLLM's metadata holds the
+    # sequence lengths on the host)
+    split_plan = L.knlp_kv_decode_plan(
+        B, Hkv, Hq, D, max_context, int(np.sum(seq_lens)), FMT[cfg["kfmt"]], cfg["kgs"],
+        FMT[cfg["vfmt"]], cfg["vgs"])
     split = args.split_tokens or split_plan
     print(f"# config {c}: {cfg['name']}; planned split_tokens={split_plan}", file=sys.stderr,
           flush=True)
@@ -322,14 +489,15 @@ def main(argv=None):
     n_tok = slots.numel()
     kc = Caches(cfg["kfmt"], nb, bs, Hkv, D, cfg["kgs"], dev)
     vc = Caches(cfg["vfmt"], nb, bs, Hkv, D, cfg["vgs"], dev)
+    clip = cfg.get("clip", 0.0)
     k16 = gen_rows(n_tok, Hkv, D, 2000 + c, cfg["outliers"], dev)
-    fill(kc, k16, slots, bs)
+    fill(kc, k16, slots, bs, clip)
     kf16 = None if args.no_fp16 else Caches("fp16", nb, bs, Hkv, D, D, dev)
     if kf16 is not None:
         fill(kf16, k16, slots, bs)
     del k16
     v16 = gen_rows(n_tok, Hkv, D, 3000 + c, cfg["outliers"], dev)
-    fill(vc, v16, slots, bs)
+    fill(vc, v16, slots, bs, clip)
     vf16 = None if args.no_fp16 else Caches("fp16", nb, bs, Hkv, D, D, dev)
     if vf16 is not None:
         fill(vf16, v16, slots, bs)
@@ -402,6 +570,9 @@ def main(argv=None):
     out_int4 = out.float().cpu().numpy()
 
     alg = algorithmic_bytes(cfg, seq_lens, cfg["kfmt"], cfg["vfmt"], bs)
+    # the partial kernel reads q, K/V, the block table and seq_lens; the
+    # output is the merge's
+    alg_partial = alg - B * Hq * D * 2
     kind = K.decode_kernel_kind(Hq, Hkv, D, FMT[cfg["kfmt"]], cfg["kgs"], FMT[cfg["vfmt"]],
                                 cfg["vgs"])
 
@@ -438,23 +609,30 @@ def main(argv=None):
         print(f"# fp16 step {ms16 * 1e3:.1f} us (split {split16})", file=sys.stderr, flush=True)
         del fcopies, ws16
 
+    # ---- sustained-read ceiling: the same byte count streamed by a plain read --------
+    stream = stream_ceiling(L, alg_partial, args.copies, dev)
+    print(f"# stream ceiling {stream['us']:.1f} us for {alg_partial} bytes "
+          f"({stream['frac_of_peak']:.3f} of peak)", file=sys.stderr, flush=True)
+
     cpu = None
     parity = None
-    if not args.no_cpu_baseline and c != 4:
-        cpu, ref, s = time_cpu_baseline(cfg, q_cpu, kc, vc, bt, seq_lens, bs)
-        parity = float(np.nanmax(np.abs(out_int4[s] - ref[0])))
-        print(f"# cpu baseline {cpu['us_per_seq']:.0f} us/seq; parity max-abs {parity:.2e}",
-              file=sys.stderr, flush=True)
+    if not args.no_cpu_baseline:
+        cpu, refs = time_cpu_baseline(cfg, q_cpu, kc, vc, bt, seq_lens, bs)
+        if refs:
+            # the bar per element: 2e-3, plus half an fp16 ulp where |ref| > 2
+            err = max(float(np.max(np.abs(out_int4[s] - r))) for s, r in refs.items())
+            ok = all(bool(np.all(np.abs(out_int4[s] - r) <=
+                                 np.where(np.abs(r) <= 2.0, 2e-3, 2e-3 + 2.0 ** -10 * np.abs(r))))
+                     for s, r in refs.items())
+            parity = {"max_abs": err, "within_bar": ok, "sequences": sorted(refs)}
+            print(f"# cpu baseline {cpu['value']} GB/s ({cpu['sample']}); parity max-abs "
+                  f"{err:.2e} within bar: {ok}", file=sys.stderr, flush=True)
+        else:
+            print(f"# cpu baseline skipped: {cpu.get('skipped')}", file=sys.stderr, flush=True)
 
     step_gbs = alg / (ms_step * 1e-3) / 1e9
-    part_gbs = alg / (ms_partial * 1e-3) / 1e9
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", f"decode_cfg{c}_traffic.json")
-    if os.path.exists(tf):
-        try:
-            traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    part_gbs = alg_partial / (ms_partial * 1e-3) / 1e9
+    traffic, traffic_note = measured_traffic(c)
     rec = {
         "metric": "decode-attn us/step and achieved HBM GB/s (% of peak), INT4 vs fp16 KV",
         "value": round(step_gbs, 1),
@@ -468,8 +646,7 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4-asym-g32 KV, fp16 q, fp32 accumulate" if c != 5 else
-                 "int8 K / int4-asym V, fp16 q, fp32 accumulate",
+        "dtype": DTYPES[c],
         "data": "synthetic (seeded N(0,1) fp16, host-generated; caches filled by the "
                 "bit-exact append kernel)",
         "config": {"workload": cfg["name"], "batch": B, "q_heads": Hq, "kv_heads": Hkv,
@@ -483,10 +660,15 @@ def main(argv=None):
         "algorithmic_bytes_per_step": alg,
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(part_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "decode partial (split-K)",
-                     "avg_launch_us": round(ms_partial * 1e3, 2)},
+                     "traffic": traffic, "traffic_source": traffic_note,
+                     "kernel": "decode partial (split-K)",
+                     "algorithmic_bytes_per_launch": alg_partial,
+                     "avg_launch_us": round(ms_partial * 1e3, 2),
+                     "stream_ceiling_frac": round(stream["frac_of_peak"], 4),
+                     "frac_of_stream_ceiling": round(part_gbs / stream["GBs"], 4)},
+        "stream_ceiling": stream,
         "cpu_baseline": cpu,
-        "parity_max_abs_vs_oracle": parity,
+        "parity_vs_oracle": parity,
         **({"append": "fused into the decode launch (knlp_kv_append_decode)",
             "append_separate_us_per_step": round(ms_step_sep * 1e3, 2)}
            if ms_step_sep is not None else {}),

@@ -228,6 +228,19 @@ int knlp_int4_twos_to_offset(const void* src, int64_t src_stride_row, void* dst,
                              int64_t dst_stride_row, int64_t rows, int64_t row_bytes,
                              void* stream);
 
+/*
+ * Measurement utility (no counterpart function in the reference; its
+ * benchmark keeps a STREAM kernel for the same purpose,
+ * scripts/v35_h100_bench.py:99-139): read `bytes` (a multiple of 16) of
+ * device memory at `src` once, `blocks` workgroups each streaming one
+ * contiguous slice with 16-byte loads, and (almost never) write one word per
+ * workgroup into `sink` [blocks] uint32, which keeps the loads live.  Timing
+ * it over the decode kernel's byte count gives the sustained-read ceiling the
+ * decode is compared with.
+ */
+int knlp_hbm_read_probe(const void* src, int64_t bytes, void* sink, int32_t blocks,
+                        void* stream);
+
 /* Which decode kernel a shape dispatches to: 1 = MFMA path, 0 = VALU path,
  * negative = unsupported (status).  Lets tests and the bench report it.  The
  * MFMA path's INT8-K, INT8-V (with INT4 or INT8 K) and more-than-16-row

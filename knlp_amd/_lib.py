@@ -26,7 +26,7 @@ EXPORTS = (
     "knlp_kv_decode_split_tokens", "knlp_kv_decode_plan", "knlp_kv_decode_workspace_bytes",
     "knlp_kv_decode_partial", "knlp_kv_decode_merge", "knlp_kv_decode",
     "knlp_kv_decode_kernel_kind", "knlp_kv_append_decode", "knlp_int4_twos_to_offset",
-    "knlp_kv_decode_noalloc",
+    "knlp_kv_decode_noalloc", "knlp_hbm_read_probe",
 )
 
 
@@ -73,6 +73,7 @@ _SIGS = {
                                       _PLANE, _P, _I64, _P, _I32, _I32, _F, _I32, _P, _I32,
                                       _I64, _I64, _P]),
     "knlp_kv_decode_kernel_kind": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32]),
+    "knlp_hbm_read_probe": (_I32, [_P, _I64, _P, _I32, _P]),
     "knlp_int4_twos_to_offset": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _P]),
     "knlp_kv_append_decode": (_I32, [_P, _I32, _I64, _I64, _I32, _I32, _I32, _I32,
                                      _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _I32, _F,

@@ -14,6 +14,8 @@ int launch_append(const void* key, const void* value, int src_bf16, int64_t num_
                   hipStream_t stream);
 int launch_twos_to_offset(const void* src, int64_t src_stride, void* dst, int64_t dst_stride,
                           int64_t rows, int64_t row_bytes, hipStream_t stream);
+int launch_hbm_read_probe(const void* src, int64_t bytes, void* sink, int blocks,
+                          hipStream_t stream);
 }
 
 using namespace knlp;
@@ -241,6 +243,14 @@ int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads, int32_
   // kernel up to two 16-row head sets (on dense cache layouts)
   if (g > 8 && !mfma) return KNLP_ERR_SHAPE;
   return mfma ? 1 : 0;
+}
+
+int knlp_hbm_read_probe(const void* src, int64_t bytes, void* sink, int32_t blocks,
+                        void* stream) {
+  if (bytes <= 0 || bytes % 16 || blocks <= 0) return KNLP_ERR_SHAPE;
+  if (src == nullptr || sink == nullptr) return KNLP_ERR_ARG;
+  if (!aligned(src, 16) || !aligned(sink, 4)) return KNLP_ERR_ALIGN;
+  return launch_hbm_read_probe(src, bytes, sink, blocks, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"
