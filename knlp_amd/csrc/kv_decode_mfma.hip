@@ -636,10 +636,26 @@ __host__ __device__ constexpr int heads_per_set() { return 16 / NG; }
 
 // q, constants and accumulators of the wave serving kv head `kvh`, for the
 // head set whose first query head (within the kv head's group) is `hs`.
+// This lane's D/4 consecutive q elements (row r = col of the head set whose
+// first query head is `hs`), as raw 16-bit words; loaded apart from
+// init_wave so that a kernel can issue these loads next to its other first
+// loads and wait once for all of them.
+template <int D, int NG>
+__device__ __forceinline__ void load_q(uint4 (&qw)[D / 32], const DecodeArgs& a, int seq,
+                                       int kvh, int col, int blk, int hs = 0) {
+  const int nh = min(heads_per_set<NG>(), a.group - hs);
+  const int rows = nh * NG;
+  const int g = col < rows ? col / NG : 0;
+  const uint16_t* qp =
+      a.q + seq * a.q_stride_seq + (kvh * a.group + hs + g) * a.q_stride_head + (D / 4) * blk;
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) qw[i] = reinterpret_cast<const uint4*>(qp)[i];
+}
+
 template <int D, int NG, bool KASYM, bool VASYM, int KCH = D / 32, int NGK = NG, bool V8 = false>
 __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8>& W,
-                                          const DecodeArgs& a, int seq, int kvh, int col,
-                                          int blk, int hs = 0) {
+                                          const uint4 (&qw)[D / 32], const DecodeArgs& a,
+                                          int col, int blk, int hs = 0) {
   constexpr int NCH = D / 32;
   constexpr int GPL = 4 / NG;
   constexpr bool K8 = KCH == 2 * NCH;
@@ -659,14 +675,11 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   float qscale = 1.0f;
   {
     const int r = col;
-    const int g = r < rows ? r / NG : 0;
     const bool on = r < rows && ((D / 4) * blk) / gs == r % NG;
-    const uint16_t* qp =
-        a.q + seq * a.q_stride_seq + (kvh * G + hs + g) * a.q_stride_head + (D / 4) * blk;
     uint16_t qv[D / 4];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
-      const uint4 w = reinterpret_cast<const uint4*>(qp)[i];
+      const uint4 w = qw[i];
       const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -816,7 +829,11 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   decode_append<D>(a, seq, kvh, split, seq_len, lane);
 
   WaveState<NCH, NG, KASYM, VASYM, KCH, NG, V8> W;
-  init_wave<D, NG, KASYM, VASYM, KCH, NG, V8>(W, a, seq, kvh, col, blk);
+  {
+    uint4 qw[D / 32];
+    load_q<D, NG>(qw, a, seq, kvh, col, blk);
+    init_wave<D, NG, KASYM, VASYM, KCH, NG, V8>(W, qw, a, col, blk);
+  }
 
   Addr A;
   {
@@ -1182,22 +1199,7 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   const int seq = blockIdx.y;
   const int h0 = blockIdx.z * L::kHeads;
   const int kvh = h0 + wave;
-  // every exit below is uniform over the block: all waves reach every barrier
-  const int seq_len = min(a.seq_lens[seq], a.max_context);
   const int t_begin = split * a.split_tokens;
-  if (t_begin >= seq_len) return;
-  const int t_end = min(seq_len, t_begin + a.split_tokens);
-  // the token being decoded, when the caller fused its append into this launch;
-  // the barrier orders every wave's rows before any wave copies the page
-  decode_append<D>(a, seq, kvh, split, seq_len, lane);
-  if (a.app.key != nullptr || a.app.value != nullptr) __syncthreads();
-
-  WS W[NSET];
-#pragma unroll
-  for (int s = 0; s < NSET; ++s)
-    init_wave<D, NG, KASYM, VASYM, KCH, NGK, V8>(W[s], a, seq, kvh, col, blk,
-                                                 s * heads_per_set<NG>());
-
   CoopAddr C;
   {
     const knlp_kv_plane& K = a.kp;
@@ -1256,13 +1258,38 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     C.bs_shift = a.block_shift;
   }
 
-  const int ntiles = (t_end - t_begin + 31) / 32;
+  // First loads, issued together and waited for once: seq_lens, this lane's
+  // q and the block-table window (bounded by the row's width, max_context,
+  // before seq_len is known: entries past the sequence are read, never used).
+  // Only then the tile copies, so no later wait for these loads (whose
+  // counter the copies share) holds up the copies in flight.
+  const int seq_len_raw = a.seq_lens[seq];
+  uint4 qw[NSET][D / 32];
+#pragma unroll
+  for (int s = 0; s < NSET; ++s) load_q<D, NG>(qw[s], a, seq, kvh, col, blk, s * heads_per_set<NG>());
   PageWindow PW;
+  PW.last = (a.max_context - 1) >> C.bs_shift;
+  PW.fill(C.bt, lane, t_begin >> C.bs_shift);              // waits for all three
+  // every exit below is uniform over the block: all waves reach every barrier
+  const int seq_len = min(seq_len_raw, a.max_context);
+  if (t_begin >= seq_len) return;
+  const int t_end = min(seq_len, t_begin + a.split_tokens);
   PW.last = (t_end - 1) >> C.bs_shift;
-  PW.fill(C.bt, lane, t_begin >> C.bs_shift);
+  // the token being decoded, when the caller fused its append into this launch;
+  // the barrier orders every wave's rows before any wave copies the page
+  decode_append<D>(a, seq, kvh, split, seq_len, lane);
+  if (a.app.key != nullptr || a.app.value != nullptr) __syncthreads();
+
+  const int ntiles = (t_end - t_begin + 31) / 32;
 #pragma unroll
   for (int t = 0; t < NBUF - 1; ++t)
     if (t < ntiles) coop_issue<L>(C, PW, lane, wave, t_begin + 32 * t, t_end, lds[t]);
+  // q -> matrix-core operands while the first tiles are in flight
+  WS W[NSET];
+#pragma unroll
+  for (int s = 0; s < NSET; ++s)
+    init_wave<D, NG, KASYM, VASYM, KCH, NGK, V8>(W[s], qw[s], a, col, blk,
+                                                 s * heads_per_set<NG>());
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
