@@ -232,15 +232,40 @@ struct Codes<2> {
   }
 };
 
+// fp16 V in the PV B-operand order: r[i] holds the 2 NCH halves of head-dim
+// columns 2 NCH col .. 2 NCH col + 2 NCH - 1 (NCH = D / 32 dwords) of token
+// 4 blk + i of the sub-tile, so each load of a 16-lane group covers one
+// token's head row (2 D bytes).
+template <int NCH>
+struct RowsH {
+  uint32_t r[4][NCH];
+  __device__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t stride) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (NCH == 4) {
+        const uint4 v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + i * stride, 0, 0));
+        r[i][0] = v.x; r[i][1] = v.y; r[i][2] = v.z; r[i][3] = v.w;
+      } else {
+        static_assert(NCH == 2, "fp16 V rows for D = 64 or 128");
+        const uint2 v = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off + i * stride, 0, 0));
+        r[i][0] = v.x; r[i][1] = v.y;
+      }
+    }
+  }
+};
+
 // One 16-token sub-tile in the per-lane layout.  K: KCH code dwords and NGK
 // scale halves per row (packed INT4: KCH = NCH, NGK = NG; INT8: KCH = 2 NCH
 // and NGK scale groups, 1 for one scale per row; fp16: KCH = 4 NCH, no
-// scales); V: VCH code dwords (packed INT4: NCH, INT8: 2 NCH).
+// scales); V: VCH code dwords (packed INT4: NCH, INT8: 2 NCH), or VCH = 0 for
+// fp16 V rows (RowsH, no scales).
 template <int NCH, int NG, int KCH = NCH, int NGK = NG, int VCH = NCH>
 struct SubTile {
-  using VCodes = Codes<VCH>;
+  using VCodes = typename std::conditional<VCH == 0, RowsH<NCH>, Codes<VCH == 0 ? 4 : VCH>>::type;
   Codes<KCH> k;
-  Codes<VCH> v;
+  VCodes v;
   Halves<NGK> ks;
   Halves<NG> kz, vs, vz;
 };
@@ -258,6 +283,7 @@ struct Addr {
   int64_t kc_b, kc_p, vc_b, vc_p;       // bytes per block / per page slot
   int64_t ks_b, ks_p, kz_b, kz_p, vs_b, vs_p, vz_b, vz_p;   // halves
   uint32_t lkc, lvc;                    // lane byte offsets of the codes
+  uint32_t vrow;                        // fp16 V: bytes from one token row to the next
   uint32_t lks, lkz, lvs, lvz;          // lane byte offsets of scales / zeros
   const int32_t* bt;
   int bs_shift;
@@ -291,10 +317,13 @@ __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane,
   const int64_t page = P.page(A.bt, lane, pbase >> A.bs_shift);
   const int64_t off0 = pbase & ((1 << A.bs_shift) - 1);
   st.k.load(rsrc_of(A.kc + (page * A.kc_b + off0 * A.kc_p)), A.lkc);
-  st.v.load(rsrc_of(A.vc + (page * A.vc_b + off0 * A.vc_p)), A.lvc);
+  if constexpr (VCH == 0)         // fp16 V rows, no scales
+    st.v.load(rsrc_of(A.vc + (page * A.vc_b + off0 * A.vc_p)), A.lvc, A.vrow);
+  else
+    st.v.load(rsrc_of(A.vc + (page * A.vc_b + off0 * A.vc_p)), A.lvc);
   if constexpr (KCH != 4 * NCH)   // fp16 K has no scales
     st.ks.load(rsrc_of(A.ks + (page * A.ks_b + off0 * A.ks_p)), A.lks);
-  st.vs.load(rsrc_of(A.vs + (page * A.vs_b + off0 * A.vs_p)), A.lvs);
+  if constexpr (VCH != 0) st.vs.load(rsrc_of(A.vs + (page * A.vs_b + off0 * A.vs_p)), A.lvs);
   if constexpr (KASYM) st.kz.load(rsrc_of(A.kz + (page * A.kz_b + off0 * A.kz_p)), A.lkz);
   if constexpr (VASYM) st.vz.load(rsrc_of(A.vz + (page * A.vz_b + off0 * A.vz_p)), A.lvz);
 }
@@ -307,7 +336,8 @@ __device__ __forceinline__ void load_sub(const Addr& A, PageWindow& P, int lane,
 // the general path: masked scores, raise_max, masked accumulate.  Both paths
 // do the same arithmetic on rows whose max does not move, so the result does
 // not depend on which path a tile took.
-template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH, int NGK = NG, bool V8 = false>
+template <int NCH, int NG, bool KASYM, bool VASYM, int KCH = NCH, int NGK = NG, bool V8 = false,
+          bool V16 = false>
 struct WaveState {
   static constexpr int GPL = 4 / NG;
   static constexpr int NGV = NG;       // V scale groups per token
@@ -318,7 +348,8 @@ struct WaveState {
   static constexpr bool K8 = KCH == 2 * NCH;
   // fp16 K: four dwords of halves per QK chunk, used as they are (no scale)
   static constexpr bool K16 = KCH == 4 * NCH;
-  using ST = SubTile<NCH, NG, KCH, NGK, V8 ? 2 * NCH : NCH>;
+  // fp16 V (V16): no scales or zero-points, values used as they are
+  using ST = SubTile<NCH, NG, KCH, NGK, V16 ? 0 : V8 ? 2 * NCH : NCH>;
   static constexpr bool KZ_USED = KASYM;
   static constexpr bool VZ_USED = VASYM;
   static_assert(NG % NGK == 0 && (K8 || K16 || NGK == NG),
@@ -381,7 +412,7 @@ struct WaveState {
     for (int x = 0; x < 2; ++x)
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
-        sv[x][g] = st[x].vs.get(g);
+        sv[x][g] = V16 ? 1.0f : st[x].vs.get(g);
         if constexpr (MASK) sv[x][g] = valid[x] ? sv[x][g] : 0.0f;
       }
   }
@@ -464,7 +495,9 @@ struct WaveState {
       for (int e = 0; e < 4; ++e) {
         sv[e] = svt[x][e % NG];
         P[e] = p[e / NG] * sv[e];
-        if constexpr (VASYM) {
+        if constexpr (V16) {
+          // fp16 V: no zero-point term
+        } else if constexpr (VASYM) {
           float zv = st[x].vz.get(e % NG);
           if constexpr (MASK) zv = valid[x] ? zv : 0.0f;
           zacc[e] = fmaf(p[e / NG], zv, zacc[e]);
@@ -531,6 +564,44 @@ struct WaveState {
         bw[1] = static_cast<uint32_t>(ta[2]) | (static_cast<uint32_t>(ta[3]) << 16);
         bw[2] = static_cast<uint32_t>(tb[0]) | (static_cast<uint32_t>(tb[1]) << 16);
         bw[3] = static_cast<uint32_t>(tb[2]) | (static_cast<uint32_t>(tb[3]) << 16);
+        const h8 bv = __builtin_bit_cast(h8, bw);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
+      }
+    }
+  }
+
+  // PV with fp16 V rows (RowsH): r[i] of sub-tile x holds columns
+  // (D/16) col .. (D/16) col + D/16 - 1 of token 16x + 4blk + i, the token of
+  // A slot 4x + i.  Accumulator j = 2c + h holds column (D/16) col + j; its B
+  // operand takes half j of each token's row, two tokens per dword with one
+  // v_perm.  Tokens past the end read 0 (their bytes are stale and could be
+  // Inf or NaN, which a zero probability would not cancel).
+  template <bool MASK>
+  __device__ __forceinline__ void pv_rows16(const ST (&st)[2], const bool (&valid)[2],
+                                            int tbase, int t_end, int blk, const h8& ahi,
+                                            const h8& alo) {
+    uint32_t r[2][4][NCH];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = !MASK || tbase + 16 * x + 4 * blk + i < t_end;
+#pragma unroll
+        for (int w = 0; w < NCH; ++w) r[x][i][w] = ok ? st[x].v.r[i][w] : 0u;
+      }
+    (void)valid;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * c + h;
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        u4 bw;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bw[q] = __builtin_amdgcn_perm(r[q / 2][2 * (q % 2) + 1][j >> 1],
+                                        r[q / 2][2 * (q % 2)][j >> 1], sel);
         const h8 bv = __builtin_bit_cast(h8, bw);
         acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
         acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
@@ -625,7 +696,11 @@ struct WaveState {
     if (slow_tile(score, sv)) slow_step(score, sv);
     h8 ahi, alo;
     probs<MASK>(st, valid, score, sv, ahi, alo);
-    pv_transposed(st, ahi, alo);
+    if constexpr (V16)
+      pv_rows16<MASK>(st, valid, tbase, t_end, static_cast<int>((threadIdx.x & (kWave - 1)) >> 4),
+                      ahi, alo);
+    else
+      pv_transposed(st, ahi, alo);
   }
 
 };
@@ -652,8 +727,9 @@ __device__ __forceinline__ void load_q(uint4 (&qw)[D / 32], const DecodeArgs& a,
   for (int i = 0; i < D / 32; ++i) qw[i] = reinterpret_cast<const uint4*>(qp)[i];
 }
 
-template <int D, int NG, bool KASYM, bool VASYM, int KCH = D / 32, int NGK = NG, bool V8 = false>
-__device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8>& W,
+template <int D, int NG, bool KASYM, bool VASYM, int KCH = D / 32, int NGK = NG, bool V8 = false,
+          bool V16 = false>
+__device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8, V16>& W,
                                           const uint4 (&qw)[D / 32], const DecodeArgs& a,
                                           int col, int blk, int hs = 0) {
   constexpr int NCH = D / 32;
@@ -754,8 +830,8 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
 // Reduce over tokens and write the wave's partial (acc, max, sum).  COLS:
 // the accumulators follow pv_columns' column order, else pv_transposed's.
 template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false, int KCH = D / 32,
-          int NGK = NG, bool V8 = false>
-__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8>& W,
+          int NGK = NG, bool V8 = false, bool V16 = false>
+__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8, V16>& W,
                                                const DecodeArgs& a, int seq, int kvh,
                                                int split, int col, int blk, int hs = 0) {
   constexpr int NCH = D / 32;
@@ -773,8 +849,8 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
   for (int c = 0; c < NCH; ++c) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int d = COLS ? (D / 16) * col + 2 * c + h
-                         : (D / 4) * (col / 4) + 8 * c + 2 * (col % 4) + h;
+      const int d = COLS || V16 ? (D / 16) * col + 2 * c + h
+                                : (D / 4) * (col / 4) + 8 * c + 2 * (col % 4) + h;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * blk + i;
@@ -783,7 +859,8 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
           const int64_t row = (row0 + g) * a.num_splits + split;
           // pv_columns' odd INT4 columns carry a factor 16
           a.part_o[row * D + d] =
-              fmaf(W.acc[c][h][i], COLS && h && !V8 ? 0x1p20f : 0x1p24f, W.zacc[i]) * kinv;
+              fmaf(W.acc[c][h][i], V16 ? 1.0f : COLS && h && !V8 ? 0x1p20f : 0x1p24f,
+                   W.zacc[i]) * kinv;
         }
       }
     }
@@ -803,13 +880,19 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
 
 // Per-head loads: each wave fetches its own kv head's rows (any layout that
 // passes the alignment checks).  One wave per (sequence, kv head, split).
-template <int D, int NG, bool KASYM, bool VASYM, bool K16 = false, bool V8 = false>
-__global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
+// fp16 K and V (V16) keep two 32-token tiles of 256-byte rows per wave in
+// registers: 4 waves per block, so each wave may use the whole register file
+// of its SIMD lane (VGPRs and AGPRs) without spilling.
+template <int D, int NG, bool KASYM, bool VASYM, bool K16 = false, bool V8 = false,
+          bool V16 = false>
+__global__ __launch_bounds__(V16 ? 256 : 512) void decode_mfma_kernel(DecodeArgs a) {
   constexpr int NCH = D / 32;    // K-chunks of 32 along head_dim = dwords per lane
   constexpr int LB = D / 8;      // bytes of INT4 codes per lane per token
   constexpr int KCH = K16 ? 4 * NCH : NCH;   // fp16 K: D/2 bytes per lane per token
-  constexpr int VCH = V8 ? 2 * NCH : NCH;    // INT8 V: D/4 bytes per lane per token
+  // INT8 V: D/4 bytes per lane per token; fp16 V: rows (Rows16, VCH = 0)
+  constexpr int VCH = V16 ? 0 : V8 ? 2 * NCH : NCH;
   constexpr int KEB = K16 ? 2 : 1;           // K element bytes (its strides are in elements)
+  constexpr int VEB = V16 ? 2 : 1;           // V element bytes
   const int lane = threadIdx.x & (kWave - 1);
   const int col = lane & 15;
   const int blk = lane >> 4;
@@ -828,11 +911,11 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
   // the token being decoded, when the caller fused its append into this launch
   decode_append<D>(a, seq, kvh, split, seq_len, lane);
 
-  WaveState<NCH, NG, KASYM, VASYM, KCH, NG, V8> W;
+  WaveState<NCH, NG, KASYM, VASYM, KCH, NG, V8, V16> W;
   {
     uint4 qw[D / 32];
     load_q<D, NG>(qw, a, seq, kvh, col, blk);
-    init_wave<D, NG, KASYM, VASYM, KCH, NG, V8>(W, qw, a, col, blk);
+    init_wave<D, NG, KASYM, VASYM, KCH, NG, V8, V16>(W, qw, a, col, blk);
   }
 
   Addr A;
@@ -840,13 +923,13 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
     const knlp_kv_plane& K = a.kp;
     const knlp_kv_plane& V = a.vp;
     A.kc = static_cast<const uint8_t*>(K.data) + KEB * kvh * K.stride_head;
-    A.vc = static_cast<const uint8_t*>(V.data) + kvh * V.stride_head;
+    A.vc = static_cast<const uint8_t*>(V.data) + VEB * kvh * V.stride_head;
     A.ks = static_cast<const uint16_t*>(K.scales) + kvh * K.s_stride_head;
     A.vs = static_cast<const uint16_t*>(V.scales) + kvh * V.s_stride_head;
     A.kz = KASYM ? static_cast<const uint16_t*>(K.zeros) + kvh * K.z_stride_head : nullptr;
     A.vz = VASYM ? static_cast<const uint16_t*>(V.zeros) + kvh * V.z_stride_head : nullptr;
     A.kc_b = KEB * K.stride_block; A.kc_p = KEB * K.stride_page;
-    A.vc_b = V.stride_block; A.vc_p = V.stride_page;
+    A.vc_b = VEB * V.stride_block; A.vc_p = VEB * V.stride_page;
     A.ks_b = K.s_stride_block; A.ks_p = K.s_stride_page;
     A.vs_b = V.s_stride_block; A.vs_p = V.s_stride_page;
     A.kz_b = K.z_stride_block; A.kz_p = K.z_stride_page;
@@ -854,7 +937,10 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
     // a lane holds elements 32 blk .. 32 blk + 31 of its token: D/8 bytes of
     // INT4 codes or D/2 bytes of fp16
     A.lkc = static_cast<uint32_t>(KEB * col * K.stride_page + (K16 ? D / 2 : LB) * blk);
-    A.lvc = static_cast<uint32_t>(col * V.stride_page + (V8 ? D / 4 : LB) * blk);
+    // fp16 V: token 4 blk + i's columns (D/16) col .. (D/16) col + D/16 - 1 (RowsH)
+    A.lvc = V16 ? static_cast<uint32_t>(2 * (4 * blk) * V.stride_page + (D / 8) * col)
+                : static_cast<uint32_t>(col * V.stride_page + (V8 ? D / 4 : LB) * blk);
+    A.vrow = static_cast<uint32_t>(2 * V.stride_page);
     A.lks = static_cast<uint32_t>(2 * col * K.s_stride_page);
     A.lvs = static_cast<uint32_t>(2 * col * V.s_stride_page);
     A.lkz = static_cast<uint32_t>(2 * col * K.z_stride_page);
@@ -895,7 +981,7 @@ __global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeArgs a) {
     if (i + 2 < ntiles) load_tile(tb + 64, X);
     run_tile(tb + 32, Y);
   }
-  write_partials<D, NG, KASYM, VASYM, false, KCH, NG, V8>(W, a, seq, kvh, split, col, blk);
+  write_partials<D, NG, KASYM, VASYM, false, KCH, NG, V8, V16>(W, a, seq, kvh, split, col, blk);
 }
 
 // ---------------------------------------------------------------------------
@@ -1338,6 +1424,10 @@ bool mfma_supported(int group, int head_size, int k_format, int k_gs, int v_form
   const auto int4 = [](int f) { return f == KNLP_KV_INT4_SYM || f == KNLP_KV_INT4_ASYM; };
   (void)q_bf16;        // bf16 q is converted exactly in init_wave
   const bool v8 = v_format == KNLP_KV_INT8_SYM;
+  // fp16 K and V: per-head kernel, one head set (the rows are the q heads)
+  if (v_format == KNLP_KV_FP16)
+    return k_format == KNLP_KV_FP16 && (head_size == 64 || head_size == 128) && group >= 1 &&
+           group <= 16;
   if (!(int4(v_format) || v8) || v_gs <= 0) return false;
   if (head_size != 64 && head_size != 128) return false;
   if (head_size % v_gs) return false;
@@ -1412,6 +1502,18 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
       if (va) hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, true, true>), grid16, block16, 0, stream, a); \
       else hipLaunchKernelGGL((decode_mfma_kernel<D, NG, false, false, true>), grid16, block16, 0, stream, a); \
       return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;                 \
+    }
+    if (a.vp.format == KNLP_KV_FP16) {   // fp16 K and V: at most 4 waves per block
+      const int h4 = min(4, heads_per_block_mfma(a.num_kv_heads));
+      const dim3 grid4(a.num_splits, a.num_seqs, a.num_kv_heads / h4);
+      const dim3 block4(kWave * h4);
+      if (head_size == 128)
+        hipLaunchKernelGGL((decode_mfma_kernel<128, 1, false, false, true, false, true>), grid4, block4, 0, stream, a);
+      else if (head_size == 64)
+        hipLaunchKernelGGL((decode_mfma_kernel<64, 1, false, false, true, false, true>), grid4, block4, 0, stream, a);
+      else
+        return KNLP_ERR_SHAPE;
+      return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
     }
     if (v8 && head_size == 128 && ng == 4) {
       hipLaunchKernelGGL((decode_mfma_kernel<128, 4, false, false, true, true>), grid16, block16, 0, stream, a);

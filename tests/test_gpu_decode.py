@@ -139,6 +139,11 @@ CASES = [
     ("kfp16_vint4_row", [800], 32, 8, 128, 3, 1, 128, 128),
     ("kfp16_vint8_row", [700, 3], 32, 8, 128, 3, 2, 128, 128),
     ("kfp16_vint8_hkv4", [450, 33], 16, 4, 128, 3, 2, 128, 32),
+    # fp16 K and V on the per-head matrix-core kernel (4 waves per block)
+    ("fp16_fp16_hkv4_g5", [900, 47, 1], 20, 4, 128, 3, 3, 128, 128),
+    ("fp16_fp16_d64", [700, 16], 16, 8, 64, 3, 3, 64, 64),
+    ("fp16_fp16_mha", [333], 6, 6, 128, 3, 3, 128, 128),
+    ("fp16_fp16_d256_valu", [400], 32, 8, 256, 3, 3, 256, 256),
 ]
 
 
@@ -306,7 +311,10 @@ def test_kernel_kind_dispatch():
     assert kk(32, 8, 64, _lib.KV_INT8_SYM, 64, _lib.KV_INT8_SYM, 32) == "valu"
     assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT4_ASYM, 32) == "mfma"
     assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_INT8_SYM, 32) == "mfma"
-    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_FP16, 128) == "valu"
+    # fp16 K and V: the matrix-core kernel (the like-for-like fp16 comparison)
+    assert kk(32, 8, 128, _lib.KV_FP16, 128, _lib.KV_FP16, 128) == "mfma"
+    assert kk(16, 4, 64, _lib.KV_FP16, 0, _lib.KV_FP16, 0) == "mfma"
+    assert kk(64, 8, 256, _lib.KV_FP16, 256, _lib.KV_FP16, 256) == "valu"
     # shapes that exist only on the cooperative kernel fall back to VALU when
     # the kv heads do not come in groups of 8
     assert kk(20, 4, 128, _lib.KV_INT4_ASYM, 32, _lib.KV_INT4_ASYM, 32) == "valu"
@@ -349,6 +357,7 @@ SMALL_V_CASES = [
     ("perhead_int4_sym_hkv4", [800, 65], 16, 4, 0, 0, 32, 32),
     ("perhead_kfp16_vint8_hkv4", [600, 17], 16, 4, 3, 2, 128, 32),
     ("perhead_kfp16_vint8_row", [600, 17], 32, 8, 3, 2, 128, 128),
+    ("perhead_fp16_fp16", [600, 17], 32, 8, 3, 3, 128, 128),
 ]
 
 
