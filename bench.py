@@ -24,7 +24,10 @@
   the plan and a few candidates (512 ... 4096 tokens) measured on the same
   inputs before timing; ``config.split_tokens_planned`` and
   ``config.split_sweep_us_per_step`` record the choice (``--no-split-sweep``
-  times the plan alone).  The fp16 leg picks its split the same way.
+  times the plan alone).  Split 0 is the stream schedule (one workgroup per
+  CU, equal shares of all rows' tiles), which the plan picks for
+  variable-length batches (config 3).  The fp16 leg picks its split the same
+  way.
 * ``stream_ceiling`` is a plain read of the partial kernel's byte count by
   the library's read probe, the best of a few launch shapes: the sustained
   HBM read rate of this GPU, beside the data-sheet 8 TB/s.
@@ -506,8 +509,10 @@ def main(argv=None):
     copies = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(args.copies - 1)]
     print(f"# inputs built: {n_tok} tokens", file=sys.stderr, flush=True)
 
-    # workspace for the smallest split tried (the largest partial count)
-    ws_bytes = L.knlp_kv_decode_workspace_bytes(B, Hq, D, max_context, 64)
+    # workspace for the smallest split tried (the largest partial count) or the
+    # stream schedule (split 0), whichever is larger
+    ws_bytes = max(L.knlp_kv_decode_workspace_bytes(B, Hq, D, max_context, 64),
+                   L.knlp_kv_decode_workspace_bytes(B, Hq, D, max_context, 0))
     ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
     out = torch.empty_like(q)
 
@@ -653,6 +658,8 @@ def main(argv=None):
                    "head_dim": D, "context": int(np.max(seq_lens)),
                    "total_tokens": int(np.sum(seq_lens)), "block_size": bs,
                    "split_tokens": split, "split_tokens_planned": split_plan,
+                   "schedule": "stream (one workgroup per CU, equal tile shares)"
+                               if split == 0 else "split-K",
                    "split_sweep_us_per_step": {str(k): round(v * 1e3, 2)
                                                for k, v in split_tried.items()},
                    "cache_copies_rotated": args.copies,
@@ -661,7 +668,8 @@ def main(argv=None):
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(part_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_source": traffic_note,
-                     "kernel": "decode partial (split-K)",
+                     "kernel": "decode partial (stream schedule)" if split == 0
+                               else "decode partial (split-K)",
                      "algorithmic_bytes_per_launch": alg_partial,
                      "avg_launch_us": round(ms_partial * 1e3, 2),
                      "stream_ceiling_frac": round(stream["frac_of_peak"], 4),

@@ -117,8 +117,21 @@ int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads,
  * knows it on the host (vLLM's metadata does) -- sizes the splits of a
  * variable-length batch from its real work; total_context <= 0 means
  * unknown (every sequence taken at max_context).  Returns the split length
- * in tokens (> 0, a multiple of 64) or a negative status.  No counterpart
- * in the reference (it has no split-K).
+ * in tokens (> 0, a multiple of 64), 0 for the stream schedule (below), or
+ * a negative status.  0 is returned for variable-length batches (total
+ * context at most 90 % of num_seqs * max_context) that the cooperative
+ * matrix-core kernel takes (Hkv % 8 == 0, INT4/INT8 K, at most 1024
+ * sequences, max_context <= 2^25).  No counterpart in the reference (it has
+ * no split-K).
+ *
+ * Stream schedule (split_tokens = 0 in the calls below): one workgroup per
+ * CU, each taking an equal share of all (sequence, group of 8 kv heads)
+ * rows' 32-token tiles laid end to end, so sequences of any mix of lengths
+ * keep every CU busy to the end; the merge folds each row's per-workgroup
+ * partials.  Its workspace depends on num_seqs, not max_context.  Planes the
+ * cooperative kernel cannot take (fp16 K, Hkv % 8 != 0, a sparse layout)
+ * run split-K inside that workspace instead.  More than 1024 sequences or
+ * max_context > 2^25 with split_tokens = 0 is KNLP_ERR_SHAPE.
  */
 int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads,
                             int32_t num_q_heads, int32_t head_size,
@@ -126,7 +139,8 @@ int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads,
                             int32_t k_format, int32_t k_group_size,
                             int32_t v_format, int32_t v_group_size);
 
-/* Bytes of fp32 workspace decode needs for this shape and split length. */
+/* Bytes of fp32 workspace decode needs for this shape and split length
+ * (split_tokens = 0: the stream schedule's). */
 int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
                                        int32_t head_size, int32_t max_context,
                                        int32_t split_tokens);

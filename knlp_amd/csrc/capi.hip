@@ -80,6 +80,10 @@ bool mfma_layout_ok(const knlp_kv_plane& P, int head_size, int block_size) {
 // Largest grid y / z extent of a HIP launch; the decode and merge launches
 // put the sequences on y.
 constexpr int kMaxGridYZ = 65535;
+// the stream schedule's blocks load every sequence's length at once (16 per
+// lane) and count 32-token tiles in 32 bits (1024 * 2^25 / 32 = 2^30)
+constexpr int kStreamMaxSeqs = 1024;
+constexpr int kStreamMaxContext = 1 << 25;
 
 // A copy of a plane in which an fp16 plane's group_size (a field it does not
 // use: it has no scales) reads head_size, so no later division sees 0.
@@ -195,8 +199,17 @@ int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads, int32_t num_
   const int64_t target = (wide ? 1LL : 2LL) * num_cus();
   // tokens over all sequences: the caller's host-side total when it has one
   // (variable-length batches), else every sequence at max_context
-  const int64_t total =
-      total_context > 0 ? total_context : static_cast<int64_t>(num_seqs) * max_context;
+  const int64_t rect = static_cast<int64_t>(num_seqs) * max_context;
+  const int64_t total = total_context > 0 ? total_context : rect;
+  // A batch whose total falls clearly short of its rectangle has sequences
+  // of different lengths: split-K leaves CUs idle at the end (the longest
+  // rows run more splits than the grid's last round holds), so the
+  // cooperative kernel's stream schedule (0) deals all rows' tiles out in
+  // equal shares instead (config 3: 180 -> 130 us).  Uniform batches keep
+  // split-K, whose start-up is about 2 us shorter.
+  if (wide && total_context > 0 && 10 * total <= 9 * rect && num_seqs <= kStreamMaxSeqs &&
+      max_context <= kStreamMaxContext)
+    return 0;
   int64_t tok = (total * hgroups + target - 1) / target;
   if (tok < 64) tok = 64;
   tok = (tok + 63) / 64 * 64;
@@ -218,8 +231,10 @@ int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads, int3
 int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t head_size,
                                        int32_t max_context, int32_t split_tokens) {
   if (num_seqs <= 0 || num_q_heads <= 0 || head_size <= 0 || max_context <= 0 ||
-      split_tokens <= 0)
+      split_tokens < 0)
     return KNLP_ERR_SHAPE;
+  if (split_tokens == 0)                       // stream schedule
+    return stream_workspace_bytes(num_seqs, num_q_heads, head_size, num_cus());
   const int ns = (max_context + split_tokens - 1) / split_tokens;
   return workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
 }
@@ -265,10 +280,15 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
                    int64_t bt_stride_seq, const int32_t* seq_lens, int32_t block_size,
                    int32_t max_context, float softmax_scale, int32_t split_tokens,
                    void* workspace, int64_t workspace_bytes, const AppendArgs* app,
-                   void* stream) {
+                   void* stream_ptr) {
   if (q_dtype != KNLP_DT_F16 && q_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
+  // split_tokens == 0: the stream schedule (one block per CU over all rows'
+  // tiles); else split-K with that many tokens per split
+  const bool stream = split_tokens == 0;
   if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
-      max_context <= 0 || split_tokens <= 0 || split_tokens % 64)
+      max_context <= 0 || split_tokens < 0 || split_tokens % 64)
+    return KNLP_ERR_SHAPE;
+  if (stream && (num_seqs > kStreamMaxSeqs || max_context > kStreamMaxContext))
     return KNLP_ERR_SHAPE;
   if (num_seqs == 0) return KNLP_OK;   // empty tensors may carry null data pointers
   if (num_seqs > kMaxGridYZ) return KNLP_ERR_SHAPE;   // one grid row per sequence
@@ -286,9 +306,11 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
   if ((st = check_plane(&vp, head_size, true))) return st;
   if (!std::isfinite(softmax_scale)) return KNLP_ERR_ARG;
   if (!aligned(query, 16) || q_stride_seq % 8 || q_stride_head % 8) return KNLP_ERR_ALIGN;
-  const int ns = (max_context + split_tokens - 1) / split_tokens;
+  const int ns = stream ? 1 : (max_context + split_tokens - 1) / split_tokens;
   if (ns > 65535) return KNLP_ERR_SHAPE;
-  const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
+  const int P = stream ? num_cus() : 0;
+  const int64_t need = stream ? stream_workspace_bytes(num_seqs, num_q_heads, head_size, P)
+                              : workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
   if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16))
     return KNLP_ERR_WORKSPACE;
 
@@ -312,13 +334,39 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
   a.num_splits = ns;
   a.max_context = max_context;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
-  workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
+  if (stream) {
+    const StreamViews v = stream_views(workspace, num_seqs, num_q_heads, head_size, P);
+    a.part_o = v.part_o;
+    a.part_ml = v.part_ml;
+    a.row_meta = v.meta;
+    a.stream_hdr = v.hdr;
+    a.stream = P;
+  } else {
+    workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
+  }
   if (app != nullptr) a.app = *app;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kind == 1 && softmax_scale > 0.0f && mfma_layout_ok(kp, head_size, block_size) &&
-      mfma_layout_ok(vp, head_size, block_size))
-    return launch_decode_mfma(a, head_size, s);
-  return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), s);
+  hipStream_t hs = static_cast<hipStream_t>(stream_ptr);
+  const bool mfma = kind == 1 && softmax_scale > 0.0f && mfma_layout_ok(kp, head_size, block_size) &&
+                    mfma_layout_ok(vp, head_size, block_size);
+  if (stream && !(mfma && stream_supported(a, head_size))) {
+    // Planes only the split schedule takes (fp16 K, Hkv % 8 != 0, a sparse
+    // layout): split-K inside the stream workspace, [num_seqs, hq, ns] over
+    // its entries, with the split recorded in its header for the merge.
+    const int64_t ns_max =
+        stream_entries(num_seqs, num_q_heads, P) / (static_cast<int64_t>(num_seqs) * num_q_heads);
+    int64_t split = (max_context + ns_max - 1) / ns_max;
+    split = (split + 63) / 64 * 64;
+    a.stream = 0;
+    a.row_meta = nullptr;
+    a.stream_hdr = nullptr;
+    a.split_tokens = static_cast<int>(split);
+    a.num_splits = static_cast<int>((max_context + split - 1) / split);
+    if (a.num_splits > kMaxGridYZ) return KNLP_ERR_SHAPE;
+    const StreamViews v = stream_views(workspace, num_seqs, num_q_heads, head_size, P);
+    if ((st = launch_stream_header(v.hdr, 0, a.split_tokens, a.num_splits, hs))) return st;
+  }
+  if (mfma) return launch_decode_mfma(a, head_size, hs);
+  return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), hs);
 }
 
 }  // namespace
@@ -344,13 +392,27 @@ int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const i
                          int32_t max_context, int32_t split_tokens, void* out, int32_t out_dtype,
                          int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
   if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
-  if (num_seqs < 0 || num_q_heads <= 0 || max_context <= 0 || split_tokens <= 0)
+  if (num_seqs < 0 || num_q_heads <= 0 || max_context <= 0 || split_tokens < 0)
     return KNLP_ERR_SHAPE;
   if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
   if (num_seqs == 0) return KNLP_OK;
   if (num_seqs > kMaxGridYZ) return KNLP_ERR_SHAPE;
   if (out == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
   if (!aligned(out, 2)) return KNLP_ERR_ALIGN;
+  if (split_tokens == 0) {                     // stream schedule
+    if (num_seqs > kStreamMaxSeqs) return KNLP_ERR_SHAPE;
+    const int P = num_cus();
+    if (workspace == nullptr ||
+        workspace_bytes < stream_workspace_bytes(num_seqs, num_q_heads, head_size, P))
+      return KNLP_ERR_WORKSPACE;
+    const StreamViews v =
+        stream_views(const_cast<void*>(workspace), num_seqs, num_q_heads, head_size, P);
+    // a row holds about P / rows + 1 entries, rows >= num_seqs
+    const int per_row = min(P, P / max(num_seqs, 1) + 2);
+    return launch_merge(v.part_o, v.part_ml, seq_lens, num_seqs, num_q_heads, head_size,
+                        max_context, 1, per_row, out, out_dtype == KNLP_DT_BF16, o_stride_seq,
+                        o_stride_head, static_cast<hipStream_t>(stream), v.meta, v.hdr);
+  }
   const int ns = (max_context + split_tokens - 1) / split_tokens;
   const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
   if (workspace == nullptr || workspace_bytes < need) return KNLP_ERR_WORKSPACE;
@@ -495,14 +557,14 @@ extern "C" int knlp_kv_decode_noalloc(const void* query, int32_t q_dtype, int64_
                                       int64_t o_stride_seq, int64_t o_stride_head,
                                       void* stream) {
   if (num_seqs < 0 || num_q_heads <= 0 || head_size <= 0 || max_context <= 0 ||
-      split_tokens <= 0)
+      split_tokens < 0)
     return KNLP_ERR_SHAPE;
   if (num_seqs == 0) return KNLP_OK;
-  const int64_t ns = (static_cast<int64_t>(max_context) + split_tokens - 1) / split_tokens;
-  if (ns > 65535) return KNLP_ERR_SHAPE;
   // every partial the merge reads is written by the partial kernel first, so
   // nothing in the scratch has to start at zero
-  const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, static_cast<int>(ns)) * 4;
+  const int64_t need = knlp_kv_decode_workspace_bytes(num_seqs, num_q_heads, head_size,
+                                                      max_context, split_tokens);
+  if (need < 0) return static_cast<int>(need);
   if (need > kScratchBytes) return KNLP_ERR_WORKSPACE;
   void* ws = device_scratch();
   if (ws == nullptr) return KNLP_ERR_LAUNCH;

@@ -42,8 +42,54 @@ struct DecodeArgs {
   float scale_log2;         // softmax_scale * log2(e)
   float* part_o;            // [num_seqs, Hq, num_splits, D]
   float* part_ml;           // [num_seqs, Hq, num_splits, 2]  (max in log2 units, sum)
+  // stream schedule (split_tokens == 0): one block per CU over the flattened
+  // tiles of all (sequence, head group) rows; partial entry
+  // (block + row) * HG + head-in-group, HG = 8 * group; row_meta[row] =
+  // (first block, block count); stream_hdr[0] = HG (read by the merge)
+  int stream;
+  int32_t* row_meta;
+  int32_t* stream_hdr;
   AppendArgs app;
 };
+
+// Stream schedule workspace: header (4 int32), row metadata, then the partials
+// of at most (blocks + num_seqs) * hq entries.  Rows are (sequence, group of 8
+// kv heads) pairs, at most num_seqs * ceil(hq / 8).
+struct StreamViews {
+  int32_t* hdr;
+  int32_t* meta;
+  float* part_ml;
+  float* part_o;
+};
+
+inline int64_t stream_entries(int num_seqs, int hq, int blocks) {
+  return (static_cast<int64_t>(blocks) + num_seqs) * hq;
+}
+
+inline int64_t stream_meta_ints(int num_seqs, int hq) {
+  return (2 * static_cast<int64_t>(num_seqs) * ((hq + 7) / 8) + 3) / 4 * 4;
+}
+
+inline int64_t stream_workspace_bytes(int num_seqs, int hq, int d, int blocks) {
+  return 16 + 4 * stream_meta_ints(num_seqs, hq) + stream_entries(num_seqs, hq, blocks) * (d + 2) * 4;
+}
+
+// Header of a stream workspace: hdr[0] = query heads per row (> 0) when the
+// stream schedule ran; hdr[0] = 0 when the planes sent the call to split-K
+// instead, with hdr[1] = split_tokens and hdr[2] = splits, the partials then
+// [num_seqs, hq, splits] over the entries.  One small kernel writes it (no
+// memset: the call may be captured in a graph).
+int launch_stream_header(int32_t* hdr, int h0, int h1, int h2, hipStream_t stream);
+
+inline StreamViews stream_views(void* ws, int num_seqs, int hq, int d, int blocks) {
+  StreamViews v;
+  v.hdr = static_cast<int32_t*>(ws);
+  v.meta = v.hdr + 4;
+  v.part_ml = reinterpret_cast<float*>(v.meta + stream_meta_ints(num_seqs, hq));
+  v.part_o = v.part_ml + 2 * stream_entries(num_seqs, hq, blocks);
+  (void)d;
+  return v;
+}
 
 // Fused append: the workgroup whose split holds position seq_len - 1 (the
 // token being decoded, whose slot the caller passes) quantises that token's
@@ -53,12 +99,10 @@ struct DecodeArgs {
 // a wave of the same workgroup after a barrier, sees them (one CU, one
 // write-through L1).  No other workgroup reads that position.
 template <int D>
-__device__ __forceinline__ void decode_append(const DecodeArgs& a, int seq, int kvh, int split,
-                                              int seq_len, int lane) {
+__device__ __forceinline__ void decode_append_if(const DecodeArgs& a, int seq, int kvh,
+                                                 bool holds_last, int lane) {
   const AppendArgs& p = a.app;
-  if ((p.key == nullptr && p.value == nullptr) || seq_len <= 0 ||
-      split != (seq_len - 1) / a.split_tokens)
-    return;
+  if ((p.key == nullptr && p.value == nullptr) || !holds_last) return;
   const int64_t slot = load_slot(p.slots, p.slots64, seq);
   if (slot < 0) return;
   const int64_t blk = slot / a.block_size;
@@ -77,6 +121,12 @@ __device__ __forceinline__ void decode_append(const DecodeArgs& a, int seq, int 
     }
   }
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0): the stores have landed
+}
+
+template <int D>
+__device__ __forceinline__ void decode_append(const DecodeArgs& a, int seq, int kvh, int split,
+                                              int seq_len, int lane) {
+  decode_append_if<D>(a, seq, kvh, seq_len > 0 && split == (seq_len - 1) / a.split_tokens, lane);
 }
 
 // Workspace split into the two partial arrays.
@@ -99,6 +149,10 @@ int launch_merge(const float* part_o, const float* part_ml, const int32_t* seq_l
                  int num_seqs, int hq, int head_size, int max_context, int split_tokens,
                  int num_splits,
                  void* out, int out_bf16, int64_t o_stride_seq, int64_t o_stride_head,
-                 hipStream_t stream);
+                 hipStream_t stream, const int32_t* stream_meta = nullptr,
+                 const int32_t* stream_hdr = nullptr);
+// launches the stream schedule (one block per CU) when a.stream is set; false
+// if this shape has no cooperative kernel (the stream schedule needs it)
+bool stream_supported(const DecodeArgs& a, int head_size);
 
 }  // namespace knlp

@@ -827,13 +827,14 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   }
 }
 
-// Reduce over tokens and write the wave's partial (acc, max, sum).  COLS:
-// the accumulators follow pv_columns' column order, else pv_transposed's.
+// Reduce over tokens and write the wave's partial (acc, max, sum) for query
+// head g of the set at entry base + g * stride of the workspace.  COLS: the
+// accumulators follow pv_columns' column order, else pv_transposed's.
 template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false, int KCH = D / 32,
           int NGK = NG, bool V8 = false, bool V16 = false>
-__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8, V16>& W,
-                                               const DecodeArgs& a, int seq, int kvh,
-                                               int split, int col, int blk, int hs = 0) {
+__device__ __forceinline__ void write_partials_at(
+    WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8, V16>& W, const DecodeArgs& a,
+    int64_t base, int64_t stride, int col, int blk, int hs = 0) {
   constexpr int NCH = D / 32;
   constexpr int GPL = 4 / NG;
   const int G = min(heads_per_set<NG>(), a.group - hs);   // heads of this set
@@ -844,7 +845,6 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
   for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]) * kinv;
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.zacc[e] = row_sum16(W.zacc[e]);
-  const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * a.group + hs;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
 #pragma unroll
@@ -856,7 +856,7 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
         const int r = 4 * blk + i;
         const int g = r / NG;
         if (g < G && d / gs == r % NG) {
-          const int64_t row = (row0 + g) * a.num_splits + split;
+          const int64_t row = base + g * stride;
           // pv_columns' odd INT4 columns carry a factor 16
           a.part_o[row * D + d] =
               fmaf(W.acc[c][h][i], V16 ? 1.0f : COLS && h && !V8 ? 0x1p20f : 0x1p24f,
@@ -870,12 +870,23 @@ __device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASY
     for (int gi = 0; gi < GPL; ++gi) {
       const int g = (4 * blk) / NG + gi;
       if (g < G) {
-        const int64_t row = (row0 + g) * a.num_splits + split;
+        const int64_t row = base + g * stride;
         a.part_ml[2 * row] = W.m_run[gi] * W.sl2[gi];
         a.part_ml[2 * row + 1] = W.lsum[gi];
       }
     }
   }
+}
+
+// The split schedule's entries: [num_seqs, Hq, num_splits].
+template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false, int KCH = D / 32,
+          int NGK = NG, bool V8 = false, bool V16 = false>
+__device__ __forceinline__ void write_partials(WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8, V16>& W,
+                                               const DecodeArgs& a, int seq, int kvh,
+                                               int split, int col, int blk, int hs = 0) {
+  const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + kvh * a.group + hs;
+  write_partials_at<D, NG, KASYM, VASYM, COLS, KCH, NGK, V8, V16>(
+      W, a, row0 * a.num_splits + split, a.num_splits, col, blk, hs);
 }
 
 // Per-head loads: each wave fetches its own kv head's rows (any layout that
@@ -1094,8 +1105,11 @@ __device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, cons
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b)));
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
   const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(lds_dst))));
+  // the low 32 bits of an LDS location's flat address are its LDS offset
+  // (the aperture is the high half); an explicit flat -> LDS cast would add a
+  // null check
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_dst)));
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                :
                : "v"(voff), "s"(sb), "s"(m0)
@@ -1263,29 +1277,137 @@ __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int 
   __syncthreads();
 }
 
+// Tiles of 32 tokens in each row of sequence s: ceil(min(seq_len, max_context) / 32).
+__device__ __forceinline__ uint32_t seq_tiles(int len, int max_context) {
+  return static_cast<uint32_t>(max(0, min(len, max_context)) + 31) / 32;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave by DPP (row_shr within
+// rows of 16 lanes, then row_bcast:15 / row_bcast:31 carry the row totals
+// into the rows above), all in VALU: no LDS round trips.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  int v = static_cast<int>(x);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);    // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);    // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);    // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);    // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);   // row_bcast:15, rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);   // row_bcast:31, rows 2, 3
+  return static_cast<uint32_t>(v);
+}
+
+// Where a stream-schedule block starts: the sequence s holding flattened tile
+// f (rows of sequence s are n_s tiles long, nhg rows per sequence, laid end
+// to end in sequence order), its first tile sbase, n_s and its length; and T,
+// all rows' tiles.  The lengths of up to 64 KMAX sequences are loaded at once
+// and scanned 64 at a time; nothing here stays live in the segment loop.
+// Tile counts fit 32 bits: num_seqs * ceil(max_context / 32) < 2^31.
+struct StreamStart {
+  static constexpr int KMAX = 16;    // up to 1024 sequences
+  uint64_t T, sbase;
+  uint32_t n;
+  int s, len, Pe;
+
+  __device__ __forceinline__ void find(const DecodeArgs& a, int nhg, int b, int P, int lane,
+                                       uint64_t* f0, uint64_t* f1) {
+    const int nk = (a.num_seqs + kWave - 1) / kWave;
+    int len_k[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int i = kWave * k + lane;
+      len_k[k] = (k < nk && i < a.num_seqs) ? a.seq_lens[i] : 0;
+    }
+    uint32_t incl[KMAX];
+    uint64_t total = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      incl[k] = 0;
+      if (k < nk) {                                           // uniform
+        incl[k] = wave_incl_scan(seq_tiles(len_k[k], a.max_context));
+        total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[k]), 63));
+      }
+    }
+    T = static_cast<uint64_t>(nhg) * total;
+    // Pe = min(P, T) blocks take part, each at least one tile, so the blocks
+    // holding one row's tiles are consecutive with no idle block among them
+    // (the merge reads one entry per block from a row's first block on)
+    Pe = static_cast<int>(min(static_cast<uint64_t>(P), T));
+    *f0 = *f1 = 0;
+    if (b >= Pe) return;
+    const uint64_t f = static_cast<uint64_t>(b) * T / Pe;
+    // the chunk holding f, then the lane within it
+    uint64_t acc = 0;
+    int kstar = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const uint64_t csum =
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[k]), 63));
+      if (k == kstar && k + 1 < nk && static_cast<uint64_t>(nhg) * (acc + csum) <= f) {
+        acc += csum;
+        kstar = k + 1;
+      }
+    }
+    int lk = 0;
+    uint32_t ik = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k == kstar) {
+        lk = len_k[k];
+        ik = incl[k];
+      }
+    }
+    // lanes whose sequence's rows all end at or before f: a prefix of the chunk
+    const int c = __popcll(__ballot(static_cast<uint64_t>(nhg) * (acc + ik) <= f));
+    if (c >= kWave) return;                                   // (cannot happen: f < T)
+    s = kWave * kstar + c;
+    len = __builtin_amdgcn_readlane(lk, c);
+    n = seq_tiles(len, a.max_context);
+    if (s >= a.num_seqs || n == 0) return;                    // (cannot happen either)
+    sbase = static_cast<uint64_t>(nhg) *
+            (acc + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ik), c)) - n);
+    *f0 = f;
+    *f1 = static_cast<uint64_t>(b + 1) * T / Pe;
+  }
+};
+
 // One block per CU (8 waves), L::NBUF tile buffers of LDS: the copies run
 // NBUF - 1 tiles ahead of the compute.  K8: INT8 K codes with NGK scale
 // groups; NSET head sets per wave.
-template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_mfma_coop_kernel(DecodeArgs a) {
+//
+// Schedules.  Split (a.stream == 0): block (split, seq, head group) runs the
+// tokens [split * split_tokens, ...) of one sequence.  Stream (a.stream = P):
+// the grid is one block per CU, and block b < Pe = min(P, T) runs the tiles
+// [b T / Pe, (b + 1) T / Pe) of all (sequence, head group) rows laid end to
+// end (T tiles of 32 tokens in all): equal work per block whatever the
+// sequence lengths, one partial per (block, row) segment, at entry
+// (b + row) * HG + head, a number no two segments share (b + row is strictly
+// increasing along the flattened tiles).  The block holding a row's first
+// tile records (first block, block count) for the merge.
+
+// One segment: tokens [t_begin, t_begin + seg_tokens) (cut at the sequence's
+// length) of sequence `seq`, kv heads 8 hg .. 8 hg + 7.  seq_len < 0: load it
+// here (together with q and the block table).  Partial of head set s, query
+// head g of this wave at entry base(s) + g * stride, base(s) = base0 +
+// s * heads_per_set.  Returns without work (uniformly) when the segment is
+// empty.
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8>
+__device__ __forceinline__ void coop_segment(const DecodeArgs& a,
+                                             uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8>::NBUF]
+                                                           [CoopLayout<D, NG, K8, NGK, V8>::BYTES],
+                                             int seq, int hg, int t_begin, int seg_tokens,
+                                             int seq_len_known, int64_t base0, int64_t stride) {
   using L = CoopLayout<D, NG, K8, NGK, V8>;
   constexpr int NCH = D / 32;
   constexpr int KCH = K8 ? 2 * NCH : NCH;
   constexpr int NBUF = L::NBUF;
   using WS = WaveState<NCH, NG, KASYM, VASYM, KCH, NGK, V8>;
-  static_assert(!(K8 && KASYM) && !(V8 && VASYM), "INT8 codes are symmetric");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][L::BYTES];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int col = lane & 15;
   const int blk = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int split = blockIdx.x;
-  const int seq = blockIdx.y;
-  const int h0 = blockIdx.z * L::kHeads;
+  const int h0 = hg * L::kHeads;
   const int kvh = h0 + wave;
-  const int t_begin = split * a.split_tokens;
   CoopAddr C;
   {
     const knlp_kv_plane& K = a.kp;
@@ -1344,12 +1466,13 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
     C.bs_shift = a.block_shift;
   }
 
-  // First loads, issued together and waited for once: seq_lens, this lane's
-  // q and the block-table window (bounded by the row's width, max_context,
-  // before seq_len is known: entries past the sequence are read, never used).
-  // Only then the tile copies, so no later wait for these loads (whose
-  // counter the copies share) holds up the copies in flight.
-  const int seq_len_raw = a.seq_lens[seq];
+  // First loads, issued together and waited for once: seq_lens (split
+  // schedule), this lane's q and the block-table window (bounded by the
+  // row's width, max_context, before seq_len is known: entries past the
+  // sequence are read, never used).  Only then the tile copies, so no later
+  // wait for these loads (whose counter the copies share) holds up the
+  // copies in flight.
+  const int seq_len_raw = seq_len_known >= 0 ? seq_len_known : a.seq_lens[seq];
   uint4 qw[NSET][D / 32];
 #pragma unroll
   for (int s = 0; s < NSET; ++s) load_q<D, NG>(qw[s], a, seq, kvh, col, blk, s * heads_per_set<NG>());
@@ -1359,11 +1482,11 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
   // every exit below is uniform over the block: all waves reach every barrier
   const int seq_len = min(seq_len_raw, a.max_context);
   if (t_begin >= seq_len) return;
-  const int t_end = min(seq_len, t_begin + a.split_tokens);
+  const int t_end = min(seq_len, t_begin + seg_tokens);
   PW.last = (t_end - 1) >> C.bs_shift;
   // the token being decoded, when the caller fused its append into this launch;
   // the barrier orders every wave's rows before any wave copies the page
-  decode_append<D>(a, seq, kvh, split, seq_len, lane);
+  decode_append_if<D>(a, seq, kvh, t_end == seq_len, lane);
   if (a.app.key != nullptr || a.app.value != nullptr) __syncthreads();
 
   const int ntiles = (t_end - t_begin + 31) / 32;
@@ -1399,9 +1522,153 @@ void decode_mfma_coop_kernel(DecodeArgs a) {
 #pragma unroll
   for (int s = 0; s < NSET; ++s) {
     W[s].pv_columns(vw, ahi[s], alo[s]);
-    write_partials<D, NG, KASYM, VASYM, true, KCH, NGK, V8>(W[s], a, seq, kvh, split, col, blk,
-                                                            s * heads_per_set<NG>());
+    write_partials_at<D, NG, KASYM, VASYM, true, KCH, NGK, V8>(
+        W[s], a, base0 + s * heads_per_set<NG>() * stride, stride, col, blk,
+        s * heads_per_set<NG>());
   }
+}
+
+// The stream schedule's walk over the flattened tiles: the next tile f, the
+// block's end fe, all tiles T, the current sequence s (its rows start at
+// tile sbase and are n tiles long; len tokens) and the blocks taking part
+// Pe.  Held in VGPRs through each segment's tile loop (hold()): as uniform
+// values the compiler would keep them in SGPRs, which the tile loop needs
+// all of; uniform() reads them back at segment boundaries.
+struct StreamWalk {
+  uint64_t f, fe, T, sbase;
+  uint32_t n;
+  int s, len, Pe;
+
+  __device__ __forceinline__ void hold() {
+    asm volatile("" : "+v"(f), "+v"(fe), "+v"(T), "+v"(sbase));
+    asm volatile("" : "+v"(n), "+v"(s), "+v"(len), "+v"(Pe));
+  }
+  __device__ __forceinline__ static uint64_t u64(uint64_t x) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+    const uint32_t hi =
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x >> 32)));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+  }
+  __device__ __forceinline__ StreamWalk uniform() const {
+    StreamWalk u;
+    u.f = u64(f);
+    u.fe = u64(fe);
+    u.T = u64(T);
+    u.sbase = u64(sbase);
+    u.n = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(n)));
+    u.s = __builtin_amdgcn_readfirstlane(s);
+    u.len = __builtin_amdgcn_readfirstlane(len);
+    u.Pe = __builtin_amdgcn_readfirstlane(Pe);
+    return u;
+  }
+};
+
+// The two schedules are separate kernels (each with its own register
+// allocation: the stream loop's state would otherwise cost the split kernel
+// registers through its whole tile loop).
+template <bool STREAM, int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8>
+__device__ __forceinline__ void coop_kernel_body(
+    const DecodeArgs& a,
+    uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8>::NBUF][CoopLayout<D, NG, K8, NGK, V8>::BYTES]) {
+  using L = CoopLayout<D, NG, K8, NGK, V8>;
+  static_assert(!(K8 && KASYM) && !(V8 && VASYM), "INT8 codes are symmetric");
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  if constexpr (!STREAM) {
+    const int split = blockIdx.x;
+    const int seq = blockIdx.y;
+    const int hg = blockIdx.z;
+    const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + (hg * L::kHeads + wave) * a.group;
+    coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(
+        a, lds, seq, hg, split * a.split_tokens, a.split_tokens, -1,
+        row0 * a.num_splits + split, a.num_splits);
+  } else {
+    // stream schedule
+    StreamWalk W;
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const int b = blockIdx.x;
+    {
+      const int nhg = a.num_kv_heads / L::kHeads;
+      if (b == 0 && threadIdx.x == 0) a.stream_hdr[0] = L::kHeads * a.group;
+      StreamStart st;
+      uint64_t f0, f1;
+      st.find(a, nhg, b, gridDim.x, lane, &f0, &f1);
+      if (f0 >= f1) return;                                   // uniform: no tiles here
+      W.f = f0;
+      W.fe = f1;
+      W.T = st.T;
+      W.sbase = st.sbase;
+      W.n = st.n;
+      W.s = st.s;
+      W.len = st.len;
+      W.Pe = st.Pe;
+    }
+    while (true) {                                            // uniform
+      // this segment's uniform view of the walk (kept in VGPRs between segments)
+      const StreamWalk U = W.uniform();
+      const int nhg = a.num_kv_heads / L::kHeads;
+      const int HG = L::kHeads * a.group;
+      const int hg = static_cast<int>((U.f - U.sbase) / U.n);
+      if (hg >= nhg) break;                                   // (cannot happen)
+      const uint64_t srow = U.sbase + static_cast<uint64_t>(hg) * U.n;
+      const uint64_t send = min(U.fe, srow + U.n);
+      const int t0 = static_cast<int>(U.f - srow);
+      const int t1 = static_cast<int>(send - srow);
+      const int row = U.s * nhg + hg;
+      if (t0 == 0 && threadIdx.x == 0) {
+        // the block holding flattened tile t: the b with
+        // floor(b T / Pe) <= t < floor((b + 1) T / Pe)
+        const uint64_t tl = srow + U.n - 1;
+        a.row_meta[2 * row] = b;
+        a.row_meta[2 * row + 1] = static_cast<int>((tl * U.Pe + U.Pe - 1) / U.T) - b + 1;
+      }
+      W.f = send;
+      W.hold();
+      // the kernel arguments (the kernel's only argument, at offset 0 of the
+      // kernarg segment) through a pointer the compiler cannot see through:
+      // their loads stay in this iteration instead of being hoisted out of
+      // the loop and held in SGPRs through every segment
+      using KArgs = const __attribute__((address_space(4))) DecodeArgs;
+      KArgs* kp = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+      asm volatile("" : "+s"(kp));
+      const DecodeArgs& A = *(const DecodeArgs*)kp;
+      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(
+          A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
+          static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
+      StreamWalk V = W.uniform();
+      if (V.f >= V.fe) break;
+      __syncthreads();    // the next segment's copies reuse the tile buffers
+      // past this sequence's rows: the next sequence with tiles (one exists,
+      // since tiles remain before fe <= T)
+      if (V.f == V.sbase + static_cast<uint64_t>(nhg) * V.n) {
+        V.sbase = V.f;
+        V.n = 0;
+        while (V.n == 0 && V.s + 1 < a.num_seqs) {
+          ++V.s;
+          V.len = a.seq_lens[V.s];
+          V.n = seq_tiles(V.len, a.max_context);
+        }
+        if (V.n == 0) break;
+        W = V;
+      }
+      W.hold();
+    }
+  }
+}
+
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_mfma_coop_kernel(DecodeArgs a) {
+  using L = CoopLayout<D, NG, K8, NGK, V8>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::NBUF][L::BYTES];
+  coop_kernel_body<false, D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(a, lds);
+}
+
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_mfma_coop_stream_kernel(DecodeArgs a) {
+  using L = CoopLayout<D, NG, K8, NGK, V8>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::NBUF][L::BYTES];
+  coop_kernel_body<true, D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(a, lds);
 }
 
 int heads_per_block_mfma(int num_kv_heads) {
@@ -1469,6 +1736,15 @@ static bool coop_layout_ok(const knlp_kv_plane& P, int head_size, int num_kv_hea
   return true;
 }
 
+bool stream_supported(const DecodeArgs& a, int head_size) {
+  if (a.kp.format == KNLP_KV_FP16 || a.vp.format == KNLP_KV_FP16) return false;
+  if (!mfma_supported(a.group, head_size, a.kp.format, a.kp.group_size, a.vp.format,
+                      a.vp.group_size, a.q_bf16))
+    return false;
+  return coop_layout_ok(a.kp, head_size, a.num_kv_heads) &&
+         coop_layout_ok(a.vp, head_size, a.num_kv_heads);
+}
+
 int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   const int ng = head_size / a.vp.group_size;
   const bool k8 = a.kp.format == KNLP_KV_INT8_SYM;
@@ -1484,11 +1760,22 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   // with fp16 K only)
   if (!coop && (k8 || (v8 && !k16) || nset > 1))
     return launch_decode_valu(a, head_size, heads_per_block_mfma(a.num_kv_heads), stream);
+  if (a.stream && !coop) return KNLP_ERR_SHAPE;   // the stream schedule is the cooperative kernel's
   const int hpb = coop ? 8 : heads_per_block_mfma(a.num_kv_heads);
-  const dim3 grid(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
+  const dim3 grid = a.stream ? dim3(a.stream) : dim3(a.num_splits, a.num_seqs, a.num_kv_heads / hpb);
   const dim3 block(kWave * hpb);
 #define KNLP_LAUNCH(...)                                                                 \
   hipLaunchKernelGGL((__VA_ARGS__), grid, block, 0, stream, a)
+#define KNLP_LAUNCH_COOP(...)                                                            \
+  do {                                                                                   \
+    if (a.stream) KNLP_LAUNCH(decode_mfma_coop_stream_kernel<__VA_ARGS__>);              \
+    else KNLP_LAUNCH(decode_mfma_coop_kernel<__VA_ARGS__>);                              \
+  } while (0)
+#define KNLP_ASYM_COOP(D, NG, ...)                                                       \
+  if (ka && va) KNLP_LAUNCH_COOP(D, NG, true, true __VA_ARGS__);                         \
+  else if (ka) KNLP_LAUNCH_COOP(D, NG, true, false __VA_ARGS__);                         \
+  else if (va) KNLP_LAUNCH_COOP(D, NG, false, true __VA_ARGS__);                         \
+  else KNLP_LAUNCH_COOP(D, NG, false, false __VA_ARGS__);
 #define KNLP_ASYM(KERNEL, D, NG, ...)                                                     \
   if (ka && va) KNLP_LAUNCH(KERNEL<D, NG, true, true __VA_ARGS__>);                       \
   else if (ka) KNLP_LAUNCH(KERNEL<D, NG, true, false __VA_ARGS__>);                       \
@@ -1535,9 +1822,9 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
 #define KNLP_INT4(D, NG)                                                                  \
   if (!k8 && !v8 && head_size == D && ng == NG) {                                         \
     if (coop && nset == 1) {                                                              \
-      KNLP_ASYM(decode_mfma_coop_kernel, D, NG, , false, NG, 1)                           \
+      KNLP_ASYM_COOP(D, NG, , false, NG, 1)                               \
     } else if (coop) {                                                                    \
-      KNLP_ASYM(decode_mfma_coop_kernel, D, NG, , false, NG, 2)                           \
+      KNLP_ASYM_COOP(D, NG, , false, NG, 2)                               \
     } else {                                                                              \
       KNLP_ASYM(decode_mfma_kernel, D, NG)                                                \
     }                                                                                     \
@@ -1545,11 +1832,11 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   }
 #define KNLP_INT8K_SETS(NG, NGK)                                                          \
   if (nset == 1) {                                                                        \
-    if (va) KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, true, true, NGK, 1>);     \
-    else KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, false, true, NGK, 1>);       \
+    if (va) KNLP_LAUNCH_COOP(128, NG, false, true, true, NGK, 1);     \
+    else KNLP_LAUNCH_COOP(128, NG, false, false, true, NGK, 1);       \
   } else {                                                                                \
-    if (va) KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, true, true, NGK, 2>);     \
-    else KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, false, false, true, NGK, 2>);       \
+    if (va) KNLP_LAUNCH_COOP(128, NG, false, true, true, NGK, 2);     \
+    else KNLP_LAUNCH_COOP(128, NG, false, false, true, NGK, 2);       \
   }
 #define KNLP_INT8K(NG)                                                                    \
   if (k8 && !v8 && head_size == 128 && ng == NG) {                                        \
@@ -1572,8 +1859,8 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
   // INT8 V (symmetric, biased codes): K INT4 (V's groups) or INT8 (one scale
   // per row or V's groups)
 #define KNLP_V8_SETS(KA, K8, NG, NGK)                                                    \
-  if (nset == 1) KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, KA, false, K8, NGK, 1, true>); \
-  else KNLP_LAUNCH(decode_mfma_coop_kernel<128, NG, KA, false, K8, NGK, 2, true>);
+  if (nset == 1) KNLP_LAUNCH_COOP(128, NG, KA, false, K8, NGK, 1, true); \
+  else KNLP_LAUNCH_COOP(128, NG, KA, false, K8, NGK, 2, true);
 #define KNLP_V8(NG)                                                                       \
   if (v8 && head_size == 128 && ng == NG) {                                               \
     if (k8 && ngk == 1) {                                                                 \
@@ -1595,6 +1882,8 @@ int launch_decode_mfma(const DecodeArgs& a, int head_size, hipStream_t stream) {
 #undef KNLP_INT8K_SETS
 #undef KNLP_INT4
 #undef KNLP_ASYM
+#undef KNLP_ASYM_COOP
+#undef KNLP_LAUNCH_COOP
 #undef KNLP_LAUNCH
   return KNLP_ERR_SHAPE;
 }

@@ -23,7 +23,9 @@ __global__ __launch_bounds__(NW * 64) void merge_kernel(const float* __restrict_
                                                     int hq, int max_context,
                                                     int split_tokens, int num_splits,
                                                     void* __restrict__ out, int out_bf16,
-                                                    int64_t o_stride_seq, int64_t o_stride_head) {
+                                                    int64_t o_stride_seq, int64_t o_stride_head,
+                                                    const int32_t* __restrict__ stream_meta,
+                                                    const int32_t* __restrict__ stream_hdr) {
   constexpr int E = D >= kWave ? D / kWave : 1;     // elements per lane
   __shared__ float s_o[NW][D];
   __shared__ float s_m[NW], s_l[NW];
@@ -32,8 +34,26 @@ __global__ __launch_bounds__(NW * 64) void merge_kernel(const float* __restrict_
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int n_len = min(seq_lens[seq], max_context);
-  const int ns = min(num_splits, (n_len + split_tokens - 1) / split_tokens);
-  const int64_t row0 = (static_cast<int64_t>(seq) * hq + h) * num_splits;
+  // the partials of (seq, h): entries row0 + i * stride, i < ns
+  int ns;
+  int64_t row0, stride;
+  if (stream_meta == nullptr) {       // split schedule: [num_seqs, hq, num_splits]
+    ns = min(num_splits, (n_len + split_tokens - 1) / split_tokens);
+    row0 = (static_cast<int64_t>(seq) * hq + h) * num_splits;
+    stride = 1;
+  } else if (stream_hdr[0] > 0) {     // stream schedule: one entry per block segment
+    const int HG = stream_hdr[0];     // query heads per row (8 kv heads' groups)
+    const int row = seq * (hq / HG) + h / HG;
+    ns = n_len > 0 ? stream_meta[2 * row + 1] : 0;    // (a row of length 0 has no entry)
+    row0 = (static_cast<int64_t>(n_len > 0 ? stream_meta[2 * row] : 0) + row) * HG + h % HG;
+    stride = HG;
+  } else {                            // split-K in a stream workspace (header: split, splits)
+    const int st = stream_hdr[1];
+    const int nsp = stream_hdr[2];
+    ns = min(nsp, (n_len + st - 1) / st);
+    row0 = (static_cast<int64_t>(seq) * hq + h) * nsp;
+    stride = 1;
+  }
 
   // Splits are taken U at a time per wave with every load of the group issued
   // before any use, so a wave waits for about one memory round trip per
@@ -49,11 +69,12 @@ __global__ __launch_bounds__(NW * 64) void merge_kernel(const float* __restrict_
     for (int u = 0; u < U; ++u) {
       const int i = base + NW * u;
       const bool ok = i < ns;
-      mi[u] = ok ? part_ml[2 * (row0 + i)] : -INFINITY;
-      li[u] = ok ? part_ml[2 * (row0 + i) + 1] : 0.0f;
+      const int64_t ent = row0 + i * stride;
+      mi[u] = ok ? part_ml[2 * ent] : -INFINITY;
+      li[u] = ok ? part_ml[2 * ent + 1] : 0.0f;
 #pragma unroll
       for (int e = 0; e < E; ++e)
-        oi[u][e] = ok && active ? part_o[(row0 + i) * D + lane * E + e] : 0.0f;
+        oi[u][e] = ok && active ? part_o[ent * D + lane * E + e] : 0.0f;
     }
     float mn = M;
 #pragma unroll
@@ -105,21 +126,35 @@ __global__ __launch_bounds__(NW * 64) void merge_kernel(const float* __restrict_
   }
 }
 
+__global__ void stream_header_kernel(int32_t* hdr, int h0, int h1, int h2) {
+  if (threadIdx.x == 0) {
+    hdr[0] = h0;
+    hdr[1] = h1;
+    hdr[2] = h2;
+  }
+}
+
+int launch_stream_header(int32_t* hdr, int h0, int h1, int h2, hipStream_t stream) {
+  hipLaunchKernelGGL(stream_header_kernel, dim3(1), dim3(kWave), 0, stream, hdr, h0, h1, h2);
+  return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
+}
+
 int launch_merge(const float* part_o, const float* part_ml, const int32_t* seq_lens,
                  int num_seqs, int hq, int head_size, int max_context, int split_tokens,
                  int num_splits,
                  void* out, int out_bf16, int64_t o_stride_seq, int64_t o_stride_head,
-                 hipStream_t stream) {
+                 hipStream_t stream, const int32_t* stream_meta, const int32_t* stream_hdr) {
   const dim3 grid(hq, num_seqs);
   // waves per (sequence, q head): one group of U = 8 splits each up to 32
-  // splits, then 8 and 16 waves
+  // splits, then 8 and 16 waves (the stream schedule passes the entries a row
+  // has on average, at most its block count)
   const int nw = num_splits <= 32 ? 4 : num_splits <= 64 ? 8 : 16;
   const dim3 block(kWave * nw);
   switch (head_size) {
 #define KNLP_MERGE_NW(D, NW)                                                            \
     hipLaunchKernelGGL((merge_kernel<D, NW>), grid, block, 0, stream, part_o, part_ml,  \
                        seq_lens, hq, max_context, split_tokens, num_splits, out, out_bf16, \
-                       o_stride_seq, o_stride_head);
+                       o_stride_seq, o_stride_head, stream_meta, stream_hdr);
 #define KNLP_MERGE_D(D)                                                                 \
   case D:                                                                               \
     if (nw == 4) { KNLP_MERGE_NW(D, 4) }                                                \

@@ -158,9 +158,15 @@ def test_decode_plan_uses_group_sizes_and_total_context():
     legacy = L.knlp_kv_decode_split_tokens(8, 8, 32, 128, 32768, a4, a4)
     assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, a4, 32, a4, 32) == legacy
     assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 8 * 32768, a4, 32, a4, 32) == legacy
-    # a variable-length batch with half the tokens of its rectangle: shorter splits
-    var = L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 64 * 8192, a4, 32, a4, 32)
-    full = L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 0, a4, 32, a4, 32)
+    # a variable-length batch (half the tokens of its rectangle) on the
+    # cooperative kernel: the stream schedule (0)
+    assert L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 64 * 8192, a4, 32, a4, 32) == 0
+    assert L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 64 * 16384 * 95 // 100, a4, 32, a4,
+                                 32) > 0                   # nearly uniform: split-K
+    assert L.knlp_kv_decode_plan(1100, 8, 32, 128, 16384, 1100 * 8192, a4, 32, a4, 32) > 0
+    # ... and on kernels without the stream schedule (Hkv % 8 != 0): shorter splits
+    var = L.knlp_kv_decode_plan(64, 4, 16, 128, 16384, 64 * 8192, a4, 32, a4, 32)
+    full = L.knlp_kv_decode_plan(64, 4, 16, 128, 16384, 0, a4, 32, a4, 32)
     assert 64 <= var < full and var % 64 == 0
     # INT8 V with g64 runs on the VALU kernel (two workgroups per CU): half
     # the split length of the cooperative kernel's plan for the same shape
@@ -168,3 +174,27 @@ def test_decode_plan_uses_group_sizes_and_total_context():
     valu = L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, i8, 128, i8, 64)
     assert valu < coop
     assert L.knlp_kv_decode_plan(8, 7, 32, 128, 32768, 0, a4, 32, a4, 32) == _lib.ERR_SHAPE
+
+
+def test_stream_schedule_workspace_and_limits():
+    """split_tokens = 0 selects the stream schedule: its workspace is sized by
+    the sequence count, not max_context, and more than 1024 sequences is a
+    shape error before anything launches."""
+    L = _lib.lib()
+    ws = L.knlp_kv_decode_workspace_bytes(64, 32, 128, 16384, 0)
+    assert ws > 0 and ws == L.knlp_kv_decode_workspace_bytes(64, 32, 128, 1 << 20, 0)
+    assert L.knlp_kv_decode_workspace_bytes(1025, 32, 128, 16384, 0) > 0
+    assert L.knlp_kv_decode_workspace_bytes(64, 32, 128, 16384, -64) == _lib.ERR_SHAPE
+    kp, vp = _plane(), _plane()
+    st = L.knlp_kv_decode(0x10000, _lib.DT_F16, 32 * 128, 128, 1025, 32, 8, 128,
+                          ctypes.byref(kp), ctypes.byref(vp), 0x50000, 2048, 0x60000, 16,
+                          32768, 0.088, 0, 0x100000, 1 << 40, 0x70000, _lib.DT_F16,
+                          32 * 128, 128, None)
+    assert st == _lib.ERR_SHAPE
+    st = L.knlp_kv_decode_merge(0x100000, 1 << 40, 0x60000, 1025, 32, 128, 32768, 0,
+                                0x70000, _lib.DT_F16, 32 * 128, 128, None)
+    assert st == _lib.ERR_SHAPE
+    # too small a workspace for the stream layout
+    st = L.knlp_kv_decode_merge(0x100000, ws - 16, 0x60000, 64, 32, 128, 16384, 0,
+                                0x70000, _lib.DT_F16, 32 * 128, 128, None)
+    assert st == _lib.ERR_WORKSPACE

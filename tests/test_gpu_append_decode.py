@@ -3,7 +3,7 @@ launch followed by the decode launch: the caches must come out bit-identical
 and so must the decode output, for every kernel family (cooperative MFMA,
 per-head MFMA, VALU), head sizes 64/128/256, sequences of length 1, new tokens
 on a split boundary and on the first position of a tile, bf16 rows, and
-slot < 0 (nothing written)."""
+slot < 0 (nothing written), and the stream schedule (split_tokens = 0)."""
 import numpy as np
 import pytest
 import torch
@@ -37,6 +37,13 @@ CASES = [
     ("valu_kint8_g64_vint8", [420], 32, 8, 128, 2, 2, 64, 64, 256, torch.float16, "valu"),
     ("valu_d256", [333, 32], 64, 8, 256, 1, 1, 32, 32, 256, torch.float16, "valu"),
     ("bf16_rows_int4", [600, 90], 32, 8, 128, 1, 1, 32, 32, 256, torch.bfloat16, "mfma"),
+    # split 0: the stream schedule (a row's last tile can sit in any block)
+    ("stream_int4_asym", [1, 33, 1024, 2049, 65], 32, 8, 128, 1, 1, 32, 32, 0, torch.float16,
+     "mfma"),
+    ("stream_kint8_row_vint4_two_sets", [900, 17, 2], 40, 8, 128, 2, 1, 128, 32, 0,
+     torch.float16, "mfma"),
+    ("stream_kint8_vint8_d128", [700, 33, 1], 32, 8, 128, 2, 2, 128, 32, 0, torch.float16,
+     "mfma"),
 ]
 
 
