@@ -73,6 +73,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int i4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 // Raw buffer resource over [base, base + 4 GiB): every cache load is
 // "scalar descriptor + 32-bit lane byte offset", so the address arithmetic of
@@ -165,6 +166,10 @@ template <>
 struct Halves<4> {
   uint2 v;
   __device__ float get(int i) const { return h2f((i < 2 ? v.x : v.y) >> (16 * (i & 1))); }
+  __device__ _Float16 geth(int i) const {
+    return __builtin_bit_cast(_Float16,
+                              static_cast<uint16_t>((i < 2 ? v.x : v.y) >> (16 * (i & 1))));
+  }
   __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
   }
@@ -173,6 +178,9 @@ template <>
 struct Halves<2> {
   uint32_t v;
   __device__ float get(int i) const { return h2f(v >> (16 * i)); }
+  __device__ _Float16 geth(int i) const {
+    return __builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> (16 * i)));
+  }
   __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     v = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
   }
@@ -181,6 +189,7 @@ template <>
 struct Halves<1> {
   uint32_t v;
   __device__ float get(int) const { return h2f(v); }
+  __device__ _Float16 geth(int) const { return __builtin_bit_cast(_Float16, static_cast<uint16_t>(v)); }
   __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     v = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
   }
@@ -403,35 +412,50 @@ struct WaveState {
     }
   }
 
-  // V scales of the two sub-tiles as fp32; tokens past the end read 0 (their
-  // bytes are stale).
+  // V scales of the two sub-tiles, kept in fp16 (the fp32 products below take
+  // them as mixed-precision operands, so they are never converted), and their
+  // largest value; tokens past the end read 0 (their bytes are stale).
   template <bool MASK>
-  __device__ __forceinline__ void vscales(const ST (&st)[2], const bool (&valid)[2],
-                                          float (&sv)[2][NG]) const {
+  __device__ __forceinline__ float vscales(const ST (&st)[2], const bool (&valid)[2],
+                                           _Float16 (&sv)[2][NG]) const {
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
-        sv[x][g] = V16 ? 1.0f : st[x].vs.get(g);
-        if constexpr (MASK) sv[x][g] = valid[x] ? sv[x][g] : 0.0f;
+        sv[x][g] = V16 ? static_cast<_Float16>(1.0f) : st[x].vs.geth(g);
+        if constexpr (MASK) sv[x][g] = valid[x] ? sv[x][g] : static_cast<_Float16>(0.0f);
       }
-  }
-
-  __device__ __forceinline__ static float max_sv(const float (&sv)[2][NG]) {
-    float m = sv[0][0];
+    if constexpr (V16) {
+      return 1.0f;
+    } else if constexpr (MASK) {
+      float m = 0.0f;
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < 2; ++x)
 #pragma unroll
-      for (int g = 0; g < NG; ++g) m = fmaxf(m, sv[x][g]);
-    return m;
+        for (int g = 0; g < NG; ++g) m = fmaxf(m, static_cast<float>(sv[x][g]));
+      return m;
+    } else {
+      // Scales are non-negative, and non-negative fp16 values order like
+      // their bit patterns: a packed unsigned 16-bit max on the scale words.
+      const auto w = [](uint32_t u) { return __builtin_bit_cast(u16x2, u); };
+      u16x2 m;
+      if constexpr (NG == 4)
+        m = __builtin_elementwise_max(__builtin_elementwise_max(w(st[0].vs.v.x), w(st[0].vs.v.y)),
+                                      __builtin_elementwise_max(w(st[1].vs.v.x), w(st[1].vs.v.y)));
+      else if constexpr (NG == 2)
+        m = __builtin_elementwise_max(w(st[0].vs.v), w(st[1].vs.v));
+      else
+        m = u16x2{static_cast<uint16_t>(st[0].vs.v), static_cast<uint16_t>(st[1].vs.v)};
+      return static_cast<float>(
+          __builtin_bit_cast(_Float16, static_cast<uint16_t>(m[0] > m[1] ? m[0] : m[1])));
+    }
   }
 
   // Does any row's tile max exceed its running max by more than thr, or any
   // V scale exceed svlim?  No cross-lane reduction: lane-wise tests and one
   // ballot.
-  __device__ __forceinline__ bool slow_tile(const float (&score)[2][GPL],
-                                            const float (&sv)[2][NG]) const {
-    bool up = max_sv(sv) > svlim;
+  __device__ __forceinline__ bool slow_tile(const float (&score)[2][GPL], float svmax) const {
+    bool up = svmax > svlim;
 #pragma unroll
     for (int gi = 0; gi < GPL; ++gi) up |= fmaxf(score[0][gi], score[1][gi]) > m_run[gi] + thr[gi];
     return __any(up);
@@ -440,12 +464,11 @@ struct WaveState {
   // Raise the running max of the rows whose tile max exceeds it by more than
   // thr, lower k when a V scale of the tile exceeds svlim, and rescale the
   // accumulators by both factors (powers of two for k, so exact).
-  __device__ __forceinline__ void slow_step(const float (&score)[2][GPL],
-                                            const float (&sv)[2][NG]) {
+  __device__ __forceinline__ void slow_step(const float (&score)[2][GPL], float svmax) {
     // k from the largest V scale of the tile over the wave: s <= 2^e, and
     // 2^k * s <= 2^12.  k only decreases (it starts at 40, far above any
     // fp16 scale's need: fp16 scales are at least 2^-24).
-    float smax = row_max16(max_sv(sv));
+    float smax = row_max16(svmax);
     smax = fmaxf(smax, __shfl_xor(smax, 16, kWave));
     smax = fmaxf(smax, __shfl_xor(smax, 32, kWave));
     int e = 0;
@@ -479,7 +502,8 @@ struct WaveState {
   // the zero-point term, for the two sub-tiles.
   template <bool MASK>
   __device__ __forceinline__ void probs(const ST (&st)[2], const bool (&valid)[2],
-                                        const float (&score)[2][GPL], const float (&svt)[2][NG],
+                                        const float (&score)[2][GPL],
+                                        const _Float16 (&svt)[2][NG],
                                         h8& ahi, h8& alo) {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
@@ -493,8 +517,10 @@ struct WaveState {
       float sv[4], P[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        sv[e] = svt[x][e % NG];
-        P[e] = p[e / NG] * sv[e];
+        sv[e] = static_cast<float>(svt[x][e % NG]);
+        // the exact product rounded once, as p * s_v: an fma with the fp16
+        // scale as a mixed operand needs no conversion
+        P[e] = fmaf(p[e / NG], sv[e], 0.0f);
         if constexpr (V16) {
           // fp16 V: no zero-point term
         } else if constexpr (VASYM) {
@@ -691,9 +717,9 @@ struct WaveState {
     }
     float score[2][GPL];
     scores<MASK>(st, valid, score);
-    float sv[2][NG];
-    vscales<MASK>(st, valid, sv);
-    if (slow_tile(score, sv)) slow_step(score, sv);
+    _Float16 sv[2][NG];
+    const float svmax = vscales<MASK>(st, valid, sv);
+    if (slow_tile(score, svmax)) slow_step(score, svmax);
     h8 ahi, alo;
     probs<MASK>(st, valid, score, sv, ahi, alo);
     if constexpr (V16)
@@ -1265,11 +1291,11 @@ __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int 
   }
   // tile i's V replaces tile i - 1's in place once its PV has consumed it
   coop_read_v<L, D>(cur, wave, col, blk, vw);
-  float sv[2][WS::NGV];
-  W[0].template vscales<MASK>(st, valid, sv);
+  _Float16 sv[2][WS::NGV];
+  const float svmax = W[0].template vscales<MASK>(st, valid, sv);
 #pragma unroll
   for (int s = 0; s < NSET; ++s) {
-    if (W[s].slow_tile(score[s], sv)) W[s].slow_step(score[s], sv);
+    if (W[s].slow_tile(score[s], svmax)) W[s].slow_step(score[s], svmax);
     W[s].template probs<MASK>(st, valid, score[s], sv, ahi[s], alo[s]);
   }
   // copies issued after tile i + 1's: tiles i + 2 .. min(i + NBUF - 1, ntiles - 1)

@@ -70,6 +70,17 @@ def test_noalloc_matches_workspace_decode_twice():
         assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
 
 
+def test_noalloc_stream_schedule_twice():
+    # split_tokens = 0: the stream schedule's partials and row records in the
+    # scratch; the second call has fewer rows, so stale records of the first
+    # lie beyond the ones it writes
+    for i, lens in enumerate(([3000, 1500, 0, 2048, 77], [900, 33])):
+        print(f"noalloc stream call {i}: seq_lens={lens}", flush=True)
+        q, planes, bt, sl = _case(lens, 32, 8, 128, 1, 32, 97 + i)
+        ref, out = _both(q, planes, bt, sl, 8, 128, 1, 32, 0)
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+
 def test_noalloc_rejects_shapes_beyond_the_scratch():
     L = _lib.lib()
     q, planes, bt, sl = _case([64], 32, 8, 128, 1, 32, 95)
