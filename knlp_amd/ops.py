@@ -16,7 +16,11 @@ reference's behaviour:
     sizes allow e.g. per-row INT8 K (group = head_size) with g32 INT4 V;
   * ``clip_ratio`` -- defaults to OUTLIER_CLIP_RATIO like F:470;
   * ``scale`` -- defaults to 1/sqrt(head_size) as F:924 fixes it;
-  * ``split_tokens`` -- split-K length, default from the library's plan.
+  * ``split_tokens`` -- split-K length, default from the library's plan; 0 is
+    the stream schedule (equal shares of all rows' tiles per CU);
+  * ``total_context`` -- the batch's summed sequence lengths when the caller
+    knows them on the host (0: unknown); the plan picks the stream schedule
+    for variable-length batches from it.
 ``block_n`` is accepted for signature compatibility and ignored: the HIP
 kernels pick their own token tiles.
 """
@@ -285,7 +289,8 @@ def append_and_decode(query, key, value, slot_mapping, key_cache, value_cache, k
                       v_scales, block_table, seq_lens, num_kv_heads, head_size, *,
                       k_format="int4", v_format="int4", k_zeros=None, v_zeros=None,
                       asymmetric=False, k_group_size=None, v_group_size=None,
-                      clip_ratio=None, scale=None, split_tokens=None) -> torch.Tensor:
+                      clip_ratio=None, scale=None, split_tokens=None,
+                      total_context=0) -> torch.Tensor:
     """Quantise the token being decoded into the caches and decode, in the
     launches of one decode (no separate append launch).
 
@@ -307,13 +312,14 @@ def append_and_decode(query, key, value, slot_mapping, key_cache, value_cache, k
                 head_size if vf == KV_FP16 else (v_group_size or GROUP_SIZE))
     clip = OUTLIER_CLIP_RATIO if clip_ratio is None else clip_ratio
     return _decode(query, kp, vp, key_cache.shape[1], block_table, seq_lens, num_kv_heads,
-                   head_size, scale, split_tokens, append=(key, value, slot_mapping, clip))
+                   head_size, scale, split_tokens, append=(key, value, slot_mapping, clip),
+                   total_context=total_context)
 
 
 def fused_int4_decode(query, key_cache, value_cache, k_scales, v_scales, block_table, seq_lens,
                       num_kv_heads, head_size, block_n=64, k_zeros=None, v_zeros=None,
                       asymmetric=False, *, group_size=None, scale=None,
-                      split_tokens=None) -> torch.Tensor:
+                      split_tokens=None, total_context=0) -> torch.Tensor:
     """Decode attention over packed INT4 K and V (F:901-979)."""
     _require_cuda(key_cache, value_cache, k_scales, v_scales)
     gs = group_size or GROUP_SIZE
@@ -321,58 +327,61 @@ def fused_int4_decode(query, key_cache, value_cache, k_scales, v_scales, block_t
     kp = _plane(key_cache, k_scales, k_zeros, fmt, gs)
     vp = _plane(value_cache, v_scales, v_zeros, fmt, gs)
     return _decode(query, kp, vp, key_cache.shape[1], block_table, seq_lens, num_kv_heads,
-                   head_size, scale, split_tokens)
+                   head_size, scale, split_tokens, total_context=total_context)
 
 
 def kint8_vint4_decode(query, key_cache_int8, value_cache_int4, k_scales, v_scales, block_table,
                        seq_lens, num_kv_heads, head_size, block_n=64, v_zeros=None,
                        asymmetric=False, *, k_group_size=None, v_group_size=None, scale=None,
-                       split_tokens=None) -> torch.Tensor:
+                       split_tokens=None, total_context=0) -> torch.Tensor:
     """Decode with symmetric INT8 K and INT4 V (F:1496-1554)."""
     _require_cuda(key_cache_int8, value_cache_int4, k_scales, v_scales)
     kp = _plane(key_cache_int8, k_scales, None, KV_INT8_SYM, k_group_size or GROUP_SIZE)
     vp = _plane(value_cache_int4, v_scales, v_zeros,
                 KV_INT4_ASYM if asymmetric else KV_INT4_SYM, v_group_size or GROUP_SIZE)
     return _decode(query, kp, vp, key_cache_int8.shape[1], block_table, seq_lens, num_kv_heads,
-                   head_size, scale, split_tokens)
+                   head_size, scale, split_tokens, total_context=total_context)
 
 
 def kfp16_vint4_decode(query, key_cache_fp16, value_cache_int4, v_scales, block_table, seq_lens,
                        num_kv_heads, head_size, block_n=64, v_zeros=None, asymmetric=False, *,
-                       v_group_size=None, scale=None, split_tokens=None) -> torch.Tensor:
+                       v_group_size=None, scale=None, split_tokens=None,
+                       total_context=0) -> torch.Tensor:
     """Decode with fp16 K and INT4 V (F:1159-1225)."""
     _require_cuda(key_cache_fp16, value_cache_int4, v_scales)
     kp = _plane(key_cache_fp16, None, None, KV_FP16, head_size)
     vp = _plane(value_cache_int4, v_scales, v_zeros,
                 KV_INT4_ASYM if asymmetric else KV_INT4_SYM, v_group_size or GROUP_SIZE)
     return _decode(query, kp, vp, key_cache_fp16.shape[1], block_table, seq_lens, num_kv_heads,
-                   head_size, scale, split_tokens)
+                   head_size, scale, split_tokens, total_context=total_context)
 
 
 def kint8_vint8_decode(query, key_cache_int8, value_cache_int8, k_scales, v_scales, block_table,
                        seq_lens, num_kv_heads, head_size, block_n=64, *, k_group_size=None,
-                       v_group_size=None, scale=None, split_tokens=None) -> torch.Tensor:
+                       v_group_size=None, scale=None, split_tokens=None,
+                       total_context=0) -> torch.Tensor:
     """Decode with symmetric INT8 K and V (F:1796-1848)."""
     _require_cuda(key_cache_int8, value_cache_int8, k_scales, v_scales)
     kp = _plane(key_cache_int8, k_scales, None, KV_INT8_SYM, k_group_size or GROUP_SIZE)
     vp = _plane(value_cache_int8, v_scales, None, KV_INT8_SYM, v_group_size or GROUP_SIZE)
     return _decode(query, kp, vp, key_cache_int8.shape[1], block_table, seq_lens, num_kv_heads,
-                   head_size, scale, split_tokens)
+                   head_size, scale, split_tokens, total_context=total_context)
 
 
 def kfp16_vint8_decode(query, key_cache_fp16, value_cache_int8, v_scales, block_table, seq_lens,
                        num_kv_heads, head_size, block_n=64, *, v_group_size=None, scale=None,
-                       split_tokens=None) -> torch.Tensor:
+                       split_tokens=None, total_context=0) -> torch.Tensor:
     """Decode with fp16 K and symmetric INT8 V (F:1975-2028)."""
     _require_cuda(key_cache_fp16, value_cache_int8, v_scales)
     kp = _plane(key_cache_fp16, None, None, KV_FP16, head_size)
     vp = _plane(value_cache_int8, v_scales, None, KV_INT8_SYM, v_group_size or GROUP_SIZE)
     return _decode(query, kp, vp, key_cache_fp16.shape[1], block_table, seq_lens, num_kv_heads,
-                   head_size, scale, split_tokens)
+                   head_size, scale, split_tokens, total_context=total_context)
 
 
 def fp16_paged_decode(query, key_cache_fp16, value_cache_fp16, block_table, seq_lens,
-                      num_kv_heads, head_size, *, scale=None, split_tokens=None) -> torch.Tensor:
+                      num_kv_heads, head_size, *, scale=None, split_tokens=None,
+                      total_context=0) -> torch.Tensor:
     """The same split-K decode reading plain fp16 paged K and V caches.
 
     Not a reference function: it is the fp16-KV instantiation of this
@@ -382,7 +391,7 @@ def fp16_paged_decode(query, key_cache_fp16, value_cache_fp16, block_table, seq_
     kp = _plane(key_cache_fp16, None, None, KV_FP16, head_size)
     vp = _plane(value_cache_fp16, None, None, KV_FP16, head_size)
     return _decode(query, kp, vp, key_cache_fp16.shape[1], block_table, seq_lens, num_kv_heads,
-                   head_size, scale, split_tokens)
+                   head_size, scale, split_tokens, total_context=total_context)
 
 
 def decode_kernel_kind(num_heads, num_kv_heads, head_size, k_format, k_group_size, v_format,

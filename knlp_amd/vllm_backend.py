@@ -79,6 +79,9 @@ class FusedInt4AttentionMetadata:
     seq_lens: torch.Tensor
     block_table: torch.Tensor
     slot_mapping: torch.Tensor
+    # summed sequence lengths, from vLLM's host copy of seq_lens when it has one
+    # (0: unknown); sizes the decode plan without a device read-back
+    total_context: int = 0
 
 
 class FusedInt4AttentionBackend(AttentionBackend):
@@ -135,11 +138,13 @@ class FusedInt4AttentionMetadataBuilder(AttentionMetadataBuilder[FusedInt4Attent
     def build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata,
               fast_build: bool = False) -> FusedInt4AttentionMetadata:
         m = common_attn_metadata
+        host_lens = getattr(m, "seq_lens_cpu", None)
         return FusedInt4AttentionMetadata(
             num_actual_tokens=m.num_actual_tokens, max_query_len=m.max_query_len,
             query_start_loc=m.query_start_loc, max_seq_len=m.max_seq_len,
             seq_lens=m.seq_lens, block_table=m.block_table_tensor,
-            slot_mapping=m.slot_mapping)
+            slot_mapping=m.slot_mapping,
+            total_context=int(host_lens.sum()) if host_lens is not None else 0)
 
 
 class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
@@ -309,7 +314,7 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
                                                attn_metadata)
             elif config.REPLACE_CACHE or attn_metadata.max_seq_len >= config.MIN_FUSED_SEQ_LEN:
                 dout = self._fused_decode(dq, key_cache_fp16, attn_metadata.block_table,
-                                          attn_metadata.seq_lens)
+                                          attn_metadata.seq_lens, attn_metadata.total_context)
             else:
                 dout = self._paged_decode(dq, key_cache_fp16, value_cache_fp16,
                                           attn_metadata.block_table, attn_metadata.seq_lens)
@@ -352,11 +357,12 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
         return self.scale if config.FUSED_DECODE_LAYER_SCALE else None
 
     def _fused_decode(self, q: torch.Tensor, key_cache_fp16: torch.Tensor,
-                      block_table: torch.Tensor, seq_lens: torch.Tensor) -> torch.Tensor:
+                      block_table: torch.Tensor, seq_lens: torch.Tensor,
+                      total_context: int = 0) -> torch.Tensor:
         """Dispatch on (k_precision, v_precision) (F:2845-2928)."""
         c, kp, vp = self._caches, self._k_precision, self._v_precision
         common = dict(num_kv_heads=self.num_kv_heads, head_size=self.head_size,
-                      scale=self._fused_scale())
+                      scale=self._fused_scale(), total_context=total_context)
         if kp == "fp16" and vp == "int8":
             return ops.kfp16_vint8_decode(q, key_cache_fp16, c.int8_value, c.v_int8_scales,
                                           block_table, seq_lens, **common)
@@ -394,7 +400,8 @@ class FusedInt4AttentionImpl(AttentionImpl[FusedInt4AttentionMetadata]):
         return ops.append_and_decode(
             q, key, value_3d[:n], md.slot_mapping[:n], kcache, vcache, ks, vs, md.block_table,
             md.seq_lens, self.num_kv_heads, self.head_size, k_format=kp, v_format=vp,
-            k_zeros=kz, v_zeros=vz, asymmetric=asym, scale=self._fused_scale())
+            k_zeros=kz, v_zeros=vz, asymmetric=asym, scale=self._fused_scale(),
+            total_context=md.total_context)
 
     def _paged_decode(self, q, key_cache, value_cache, block_table, seq_lens) -> torch.Tensor:
         """Short sequences from the fp16 paged cache (F:2930-3048)."""

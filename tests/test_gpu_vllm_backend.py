@@ -87,7 +87,7 @@ def run_two_steps(vb, impl, dtype, prompt_lens, seed):
         query_start_loc=torch.arange(S + 1, dtype=torch.int32, device=dev),
         max_seq_len=max(prompt_lens) + 1,
         seq_lens=torch.tensor([n + 1 for n in prompt_lens], dtype=torch.int32, device=dev),
-        block_table=bt_d, slot_mapping=slots2)
+        block_table=bt_d, slot_mapping=slots2, total_context=sum(prompt_lens) + S)
     k2d, v2d = k2.to(dev).view(S, -1), v2.to(dev).view(S, -1)
     impl.do_kv_cache_update(None, k2d, v2d, kv, slots2)
     out_dec = impl.forward(None, q2.to(dev).view(S, -1), k2d, v2d, kv, md2)
@@ -227,3 +227,29 @@ def test_fused_decode_softmax_scale(vb, monkeypatch, layer_scale):
     got = r["out_dec"].float().numpy().reshape(want.shape)
     assert close(got, want)
     assert np.abs(got - other).max() > 2e-2      # the two scales give different outputs
+
+
+def test_decode_stream_schedule_through_backend(vb, monkeypatch):
+    """Hkv = 8 and a variable-length batch: with the host-side total context
+    the plan picks the stream schedule; the backend's decode still matches
+    the oracle over its shadow caches."""
+    import sys as _sys
+    mod = _sys.modules[__name__]
+    monkeypatch.setattr(mod, "H", 32)
+    monkeypatch.setattr(mod, "HKV", 8)
+    from knlp_amd import _lib
+    impl = impl_for(vb, monkeypatch, "int4", "int4", True, msl=48)
+    lens = [300, 40, 5]
+    width = max(-(-(n + 1) // BS) for n in lens)
+    assert _lib.lib().knlp_kv_decode_plan(3, 8, 32, D, width * BS, sum(lens) + 3, 1, 32, 1,
+                                          32) == 0
+    r = run_two_steps(vb, impl, torch.float16, lens, seed=300)
+    gs = config.GROUP_SIZE
+    kp = kvgen.empty_plane(1, NB, BS, 8, D, gs)
+    vp = kvgen.empty_plane(1, NB, BS, 8, D, gs)
+    for x, y, sl in ((r["k"], r["v"], r["slots"]), (r["k2"], r["v2"], r["slots2"])):
+        kvgen.fill_plane(kp, x.float().numpy(), sl, config.OUTLIER_CLIP_RATIO)
+        kvgen.fill_plane(vp, y.float().numpy(), sl, config.OUTLIER_CLIP_RATIO)
+    ref = A.decode_reference(r["q2"].float().numpy(), kp, vp, r["bt"], [n + 1 for n in lens],
+                             round_output=False)
+    assert close(r["out_dec"].float().numpy().reshape(ref.shape), ref)

@@ -132,6 +132,9 @@ def test_builder(vb):
     md = b.build(0, m)
     assert md.max_seq_len == 9 and md.max_query_len == 1 and md.num_actual_tokens == 2
     assert md.block_table is m.block_table_tensor and md.slot_mapping is m.slot_mapping
+    assert md.total_context == 0                      # no host copy of the lengths
+    m.seq_lens_cpu = torch.tensor([5, 9])
+    assert b.build(0, m).total_context == 14
 
 
 # ---- dispatch with recording operators ---------------------------------------------------------

@@ -55,3 +55,4 @@ class CommonAttentionMetadata:
     max_seq_len: int
     block_table_tensor: torch.Tensor
     slot_mapping: torch.Tensor
+    seq_lens_cpu: torch.Tensor | None = None
