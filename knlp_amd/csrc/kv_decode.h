@@ -46,7 +46,7 @@ struct DecodeArgs {
   // tiles of all (sequence, head group) rows; partial entry
   // (block + row) * HG + head-in-group, HG = 8 * group; row_meta[row] =
   // (first block, block count); stream_hdr[0] = HG (read by the merge)
-  int stream;
+  int stream;               // the block count P of the stream schedule, else 0
   int32_t* row_meta;
   int32_t* stream_hdr;
   AppendArgs app;

@@ -4,10 +4,11 @@
 // Same contract as decode_valu_kernel (kv_decode_valu.hip): unnormalised
 // partials (acc, max, sum) per (sequence, q head, split) in the workspace,
 // softmax in base 2.  Replaces the reference's _fused_int4_decode_kernel
-// (F:656-894) for these shapes.  Two kernels share the per-wave arithmetic:
+// (F:656-894) for these shapes.  Three kernels share the per-wave arithmetic:
 // decode_mfma_kernel (one wave per (sequence, kv head, split), loads straight
-// into VGPRs) and decode_mfma_coop_kernel (8 waves stage whole pages of 8 kv
-// heads through LDS; described further down).
+// into VGPRs), decode_mfma_coop_kernel (8 waves stage whole pages of 8 kv
+// heads through LDS; described further down) and decode_mfma_coop_stream_kernel
+// (the same block, one per CU, over equal shares of all rows' tiles).
 //
 // Work per wave and 32-token tile (two 16-token sub-tiles); lane l has
 // col = l % 16, blk = l / 16.  "Slot (blk, e)" is element e of lane block blk
