@@ -207,8 +207,12 @@ int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads, int32_t num_
   // cooperative kernel's stream schedule (0) deals all rows' tiles out in
   // equal shares instead (config 3: 180 -> 130 us).  Uniform batches keep
   // split-K, whose start-up is about 2 us shorter.
-  if (wide && total_context > 0 && 10 * total <= 9 * rect && num_seqs <= kStreamMaxSeqs &&
-      max_context <= kStreamMaxContext)
+  // (Two head sets with fewer than 4 V groups run out of registers in the
+  // stream kernel and stay on split-K.)
+  const int vng = v_format == KNLP_KV_FP16 || v_group_size <= 0 ? 1 : head_size / v_group_size;
+  const bool stream_fits = g * vng <= 16 || vng == 4;
+  if (wide && stream_fits && total_context > 0 && 10 * total <= 9 * rect &&
+      num_seqs <= kStreamMaxSeqs && max_context <= kStreamMaxContext)
     return 0;
   int64_t tok = (total * hgroups + target - 1) / target;
   if (tok < 64) tok = 64;

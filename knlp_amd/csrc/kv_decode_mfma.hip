@@ -1428,7 +1428,12 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
   constexpr int KCH = K8 ? 2 * NCH : NCH;
   constexpr int NBUF = L::NBUF;
   using WS = WaveState<NCH, NG, KASYM, VASYM, KCH, NGK, V8>;
-  const int tid = threadIdx.x;
+  // An opaque thread index: the stream schedule runs this once per segment
+  // in a loop, and lane-derived set-up hoisted out of that loop would stay
+  // live in VGPRs through every segment's tile loop (+50 VGPRs, and spills
+  // with two head sets); recomputing it per segment costs a few VALU.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & (kWave - 1);
   const int col = lane & 15;
   const int blk = lane >> 4;
@@ -1558,34 +1563,45 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
 // The stream schedule's walk over the flattened tiles: the next tile f, the
 // block's end fe, all tiles T, the current sequence s (its rows start at
 // tile sbase and are n tiles long; len tokens) and the blocks taking part
-// Pe.  Held in VGPRs through each segment's tile loop (hold()): as uniform
-// values the compiler would keep them in SGPRs, which the tile loop needs
-// all of; uniform() reads them back at segment boundaries.
+// Pe.  Through each segment's tile loop it lives in the lanes of one VGPR
+// (hold() returns it, field i in lane i): as uniform values the compiler would keep
+// its 12 words in SGPRs, which the tile loop needs all of, or in 12 VGPRs,
+// which a two-head-set tile loop does not have to spare; uniform() reads it
+// back at segment boundaries.
 struct StreamWalk {
   uint64_t f, fe, T, sbase;
   uint32_t n;
   int s, len, Pe;
 
-  __device__ __forceinline__ void hold() {
-    asm volatile("" : "+v"(f), "+v"(fe), "+v"(T), "+v"(sbase));
-    asm volatile("" : "+v"(n), "+v"(s), "+v"(len), "+v"(Pe));
+  // the walk in one VGPR, field i in lane i
+  __device__ __forceinline__ uint32_t hold() const {
+    const uint32_t w[12] = {static_cast<uint32_t>(f),     static_cast<uint32_t>(f >> 32),
+                            static_cast<uint32_t>(fe),    static_cast<uint32_t>(fe >> 32),
+                            static_cast<uint32_t>(T),     static_cast<uint32_t>(T >> 32),
+                            static_cast<uint32_t>(sbase), static_cast<uint32_t>(sbase >> 32),
+                            n, static_cast<uint32_t>(s), static_cast<uint32_t>(len),
+                            static_cast<uint32_t>(Pe)};
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 12; ++i) v = lane == i ? w[i] : v;
+    asm volatile("" : "+v"(v));     // opaque: reads below come from the VGPR
+    return v;
   }
-  __device__ __forceinline__ static uint64_t u64(uint64_t x) {
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
-    const uint32_t hi =
-        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x >> 32)));
-    return (static_cast<uint64_t>(hi) << 32) | lo;
-  }
-  __device__ __forceinline__ StreamWalk uniform() const {
+  __device__ __forceinline__ static StreamWalk uniform(uint32_t packed) {
+    const auto lane = [&](int i) {
+      return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(packed), i));
+    };
+    const auto u64 = [&](int i) { return (static_cast<uint64_t>(lane(i + 1)) << 32) | lane(i); };
     StreamWalk u;
-    u.f = u64(f);
-    u.fe = u64(fe);
-    u.T = u64(T);
-    u.sbase = u64(sbase);
-    u.n = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(n)));
-    u.s = __builtin_amdgcn_readfirstlane(s);
-    u.len = __builtin_amdgcn_readfirstlane(len);
-    u.Pe = __builtin_amdgcn_readfirstlane(Pe);
+    u.f = u64(0);
+    u.fe = u64(2);
+    u.T = u64(4);
+    u.sbase = u64(6);
+    u.n = lane(8);
+    u.s = static_cast<int>(lane(9));
+    u.len = static_cast<int>(lane(10));
+    u.Pe = static_cast<int>(lane(11));
     return u;
   }
 };
@@ -1610,7 +1626,7 @@ __device__ __forceinline__ void coop_kernel_body(
         row0 * a.num_splits + split, a.num_splits);
   } else {
     // stream schedule
-    StreamWalk W;
+    uint32_t walk;                  // StreamWalk::hold(): the walk's state in one VGPR
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int b = blockIdx.x;
     {
@@ -1620,6 +1636,7 @@ __device__ __forceinline__ void coop_kernel_body(
       uint64_t f0, f1;
       st.find(a, nhg, b, gridDim.x, lane, &f0, &f1);
       if (f0 >= f1) return;                                   // uniform: no tiles here
+      StreamWalk W;
       W.f = f0;
       W.fe = f1;
       W.T = st.T;
@@ -1628,10 +1645,11 @@ __device__ __forceinline__ void coop_kernel_body(
       W.s = st.s;
       W.len = st.len;
       W.Pe = st.Pe;
+      walk = W.hold();
     }
     while (true) {                                            // uniform
-      // this segment's uniform view of the walk (kept in VGPRs between segments)
-      const StreamWalk U = W.uniform();
+      // this segment's uniform view of the walk
+      const StreamWalk U = StreamWalk::uniform(walk);
       const int nhg = a.num_kv_heads / L::kHeads;
       const int HG = L::kHeads * a.group;
       const int hg = static_cast<int>((U.f - U.sbase) / U.n);
@@ -1648,8 +1666,11 @@ __device__ __forceinline__ void coop_kernel_body(
         a.row_meta[2 * row] = b;
         a.row_meta[2 * row + 1] = static_cast<int>((tl * U.Pe + U.Pe - 1) / U.T) - b + 1;
       }
-      W.f = send;
-      W.hold();
+      {
+        StreamWalk N = U;
+        N.f = send;
+        walk = N.hold();
+      }
       // the kernel arguments (the kernel's only argument, at offset 0 of the
       // kernarg segment) through a pointer the compiler cannot see through:
       // their loads stay in this iteration instead of being hoisted out of
@@ -1661,7 +1682,7 @@ __device__ __forceinline__ void coop_kernel_body(
       coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(
           A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
           static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
-      StreamWalk V = W.uniform();
+      StreamWalk V = StreamWalk::uniform(walk);
       if (V.f >= V.fe) break;
       __syncthreads();    // the next segment's copies reuse the tile buffers
       // past this sequence's rows: the next sequence with tiles (one exists,
@@ -1675,9 +1696,8 @@ __device__ __forceinline__ void coop_kernel_body(
           V.n = seq_tiles(V.len, a.max_context);
         }
         if (V.n == 0) break;
-        W = V;
       }
-      W.hold();
+      walk = V.hold();
     }
   }
 }
