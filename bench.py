@@ -94,7 +94,10 @@ DTYPES = {
 }
 # kernel sources whose code decides the partial kernel's HBM traffic; a
 # committed counter measurement counts only while they are unchanged
-TRAFFIC_SOURCES = ("knlp_amd/csrc/kv_decode_mfma.hip", "knlp_amd/csrc/kv_decode.h",
+TRAFFIC_SOURCES = ("knlp_amd/csrc/kv_decode_mfma.h", "knlp_amd/csrc/kv_decode_mfma.hip",
+                   "knlp_amd/csrc/kv_decode_mfma_coop.h", "knlp_amd/csrc/kv_decode_mfma_coop.hip",
+                   "knlp_amd/csrc/kv_decode_mfma_stream.hip",
+                   "knlp_amd/csrc/kv_decode_mfma_perhead.hip", "knlp_amd/csrc/kv_decode.h",
                    "knlp_amd/csrc/kv_quant.h", "knlp_amd/csrc/kv_common.h")
 
 
