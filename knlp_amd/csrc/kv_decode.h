@@ -44,17 +44,20 @@ struct DecodeArgs {
   float* part_ml;           // [num_seqs, Hq, num_splits, 2]  (max in log2 units, sum)
   // stream schedule (split_tokens == 0): one block per CU over the flattened
   // tiles of all (sequence, head group) rows; partial entry
-  // (block + row) * HG + head-in-group, HG = 8 * group; row_meta[row] =
-  // (first block, block count); stream_hdr[0] = HG (read by the merge)
+  // (block + row) * HG + head-in-group, HG = 8 * group; row_meta[seq * hq +
+  // q head] = (its first entry, entry count); stream_hdr[0] = HG, the stride
+  // of a q head's entries (read by the merge)
   int stream;               // the block count P of the stream schedule, else 0
   int32_t* row_meta;
   int32_t* stream_hdr;
   AppendArgs app;
 };
 
-// Stream schedule workspace: header (4 int32), row metadata, then the partials
-// of at most (blocks + num_seqs) * hq entries.  Rows are (sequence, group of 8
-// kv heads) pairs, at most num_seqs * ceil(hq / 8).
+// Stream schedule workspace: header (4 int32), per-(sequence, q head) records
+// of the partials (first entry, count), then the partials of at most
+// (blocks + num_seqs) * hq entries.  Rows are (sequence, group of 8 kv heads)
+// pairs.  The records are per q head so that the merge can load a record, the
+// header and the sequence length together, without one depending on another.
 struct StreamViews {
   int32_t* hdr;
   int32_t* meta;
@@ -67,7 +70,7 @@ inline int64_t stream_entries(int num_seqs, int hq, int blocks) {
 }
 
 inline int64_t stream_meta_ints(int num_seqs, int hq) {
-  return (2 * static_cast<int64_t>(num_seqs) * ((hq + 7) / 8) + 3) / 4 * 4;
+  return (2 * static_cast<int64_t>(num_seqs) * hq + 3) / 4 * 4;
 }
 
 inline int64_t stream_workspace_bytes(int num_seqs, int hq, int d, int blocks) {

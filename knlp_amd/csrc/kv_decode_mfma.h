@@ -1414,7 +1414,8 @@ struct StreamStart {
 // sequence lengths, one partial per (block, row) segment, at entry
 // (b + row) * HG + head, a number no two segments share (b + row is strictly
 // increasing along the flattened tiles).  The block holding a row's first
-// tile records (first block, block count) for the merge.
+// tile writes, for each q head of the row, its first entry and the count of
+// blocks holding the row for the merge.
 
 // One segment: tokens [t_begin, t_begin + seg_tokens) (cut at the sequence's
 // length) of sequence `seq`, kv heads 8 hg .. 8 hg + 7.  seq_len < 0: load it
@@ -1664,12 +1665,15 @@ __device__ __forceinline__ void coop_kernel_body(
       const int t0 = static_cast<int>(U.f - srow);
       const int t1 = static_cast<int>(send - srow);
       const int row = U.s * nhg + hg;
-      if (t0 == 0 && threadIdx.x == 0) {
-        // the block holding flattened tile t: the b with
-        // floor(b T / Pe) <= t < floor((b + 1) T / Pe)
+      if (t0 == 0 && static_cast<int>(threadIdx.x) < HG) {
+        // the row's record, one per q head j: its first entry and the count
+        // of blocks holding the row's tiles (the block holding flattened tile
+        // t: the b with floor(b T / Pe) <= t < floor((b + 1) T / Pe))
         const uint64_t tl = srow + U.n - 1;
-        a.row_meta[2 * row] = b;
-        a.row_meta[2 * row + 1] = static_cast<int>((tl * U.Pe + U.Pe - 1) / U.T) - b + 1;
+        const int j = threadIdx.x;
+        int32_t* rec = a.row_meta + 2 * (static_cast<int64_t>(U.s) * a.num_q_heads + hg * HG + j);
+        rec[0] = (b + row) * HG + j;
+        rec[1] = static_cast<int>((tl * U.Pe + U.Pe - 1) / U.T) - b + 1;
       }
       {
         StreamWalk N = U;

@@ -41,18 +41,23 @@ __global__ __launch_bounds__(NW * 64) void merge_kernel(const float* __restrict_
     ns = min(num_splits, (n_len + split_tokens - 1) / split_tokens);
     row0 = (static_cast<int64_t>(seq) * hq + h) * num_splits;
     stride = 1;
-  } else if (stream_hdr[0] > 0) {     // stream schedule: one entry per block segment
-    const int HG = stream_hdr[0];     // query heads per row (8 kv heads' groups)
-    const int row = seq * (hq / HG) + h / HG;
-    ns = n_len > 0 ? stream_meta[2 * row + 1] : 0;    // (a row of length 0 has no entry)
-    row0 = (static_cast<int64_t>(n_len > 0 ? stream_meta[2 * row] : 0) + row) * HG + h % HG;
-    stride = HG;
-  } else {                            // split-K in a stream workspace (header: split, splits)
-    const int st = stream_hdr[1];
-    const int nsp = stream_hdr[2];
-    ns = min(nsp, (n_len + st - 1) / st);
-    row0 = (static_cast<int64_t>(seq) * hq + h) * nsp;
-    stride = 1;
+  } else {
+    // a stream workspace: the record, the header and the length load
+    // together (none needs another; the record is unused after a split-K run)
+    const int64_t r = 2 * (static_cast<int64_t>(seq) * hq + h);
+    const int first = stream_meta[r], count = stream_meta[r + 1];
+    const int hg = stream_hdr[0];
+    if (hg > 0) {                     // stream schedule: one entry per block segment
+      ns = n_len > 0 ? count : 0;     // (a row of length 0 has no record)
+      row0 = n_len > 0 ? first : 0;
+      stride = hg;                    // query heads per row (8 kv heads' groups)
+    } else {                          // split-K in the workspace (header: split, splits)
+      const int st = stream_hdr[1];
+      const int nsp = stream_hdr[2];
+      ns = min(nsp, (n_len + st - 1) / st);
+      row0 = (static_cast<int64_t>(seq) * hq + h) * nsp;
+      stride = 1;
+    }
   }
 
   // Splits are taken U at a time per wave with every load of the group issued
