@@ -28,8 +28,12 @@ def _caches(seq_lens, hq, hkv, d, seed, dev):
     return planes, torch.from_numpy(bt).to(dev), q
 
 
-@pytest.mark.parametrize("hkv", [8, 4], ids=["cooperative", "per_head"])
-def test_decode_graph_replays_match_eager(hkv):
+@pytest.mark.parametrize("hkv,split", [(8, None), (4, None), (8, 0), (4, 0)],
+                         ids=["cooperative", "per_head", "stream", "stream_fallback_split_k"])
+def test_decode_graph_replays_match_eager(hkv, split):
+    """split 0: the stream schedule (its workspace records and header are
+    written by kernels, not memsets); with Hkv = 4 the planes fall back to
+    split-K inside that workspace, whose header a one-wave kernel writes."""
     dev = torch.device("cuda")
     hq, d = 4 * hkv, 128
     seq_lens = [1500, 77, 4096]
@@ -38,7 +42,8 @@ def test_decode_graph_replays_match_eager(hkv):
 
     def step():
         return K.fused_int4_decode(q, kp[0], vp[0], kp[1], vp[1], bt, sl, hkv, d,
-                                   k_zeros=kp[2], v_zeros=vp[2], asymmetric=True)
+                                   k_zeros=kp[2], v_zeros=vp[2], asymmetric=True,
+                                   split_tokens=split)
 
     want = step()
     torch.cuda.synchronize()
