@@ -137,3 +137,14 @@ def test_stream_schedule_reads_only_what_it_wrote(seq_lens):
     assert st == 0
     torch.cuda.synchronize()
     _check(out.cpu(), q.cpu(), kp, vp, bt, seq_lens, name="stream_nan_workspace")
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_stream_schedule_other_block_sizes(bs):
+    """Pages of 32 and 64 tokens: a 32-token tile then lies within one page
+    (both 16-token halves), and a row's segment can start mid-page."""
+    seq_lens = [1000, 33, 0, 517, 64]
+    bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, seed=74, bs=bs)
+    q = _query(len(seq_lens), 32, 128, 74)
+    out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=0)
+    _check(out, q, kp, vp, bt, seq_lens, name=f"stream_block_size_{bs}")
