@@ -148,3 +148,13 @@ def test_stream_schedule_other_block_sizes(bs):
     q = _query(len(seq_lens), 32, 128, 74)
     out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=0)
     _check(out, q, kp, vp, bt, seq_lens, name=f"stream_block_size_{bs}")
+
+
+def test_stream_schedule_all_sequences_empty():
+    """No tiles at all: every block returns at once and every output is NaN
+    (0/0, like the reference's acc / l with l = 0, F:886-887)."""
+    seq_lens = [0, 0, 0]
+    bt, kp, vp = _build(seq_lens, 32, 8, 128, 1, 1, 32, 32, seed=75)
+    q = _query(3, 32, 128, 75)
+    out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=0)
+    assert torch.isnan(out.float()).all()
