@@ -394,6 +394,38 @@ def fp16_paged_decode(query, key_cache_fp16, value_cache_fp16, block_table, seq_
                    head_size, scale, split_tokens, total_context=total_context)
 
 
+def decode_fp16_sdpa(query, fp16_k, fp16_v, seq_lens, num_kv_heads, num_heads,
+                     head_size) -> torch.Tensor:
+    """Decode attention over per-sequence fp16 K/V (F:2031-2071): ``fp16_k``
+    and ``fp16_v`` are ``[max_seqs, max_ctx, num_kv_heads, head_size]``,
+    sequence s holding its first ``seq_lens[s]`` positions; softmax scale
+    1/sqrt(head_size), GQA head h reading kv head h // (num_heads /
+    num_kv_heads), output shaped like ``query``.  The reference loops over
+    the sequences with SDPA on repeat_interleave-expanded K/V; here the
+    tensors are read in place as a paged cache (16-token pages when max_ctx
+    allows, else one page per sequence) by the fp16 decode kernel, with no
+    host synchronisation."""
+    _require_cuda(query, fp16_k, fp16_v, seq_lens)
+    if query.dim() != 3 or query.shape[1] != num_heads or query.shape[2] != head_size:
+        raise ValueError("query must be [num_seqs, num_heads, head_size]")
+    for t in (fp16_k, fp16_v):
+        if t.dim() != 4 or t.shape[2] != num_kv_heads or t.shape[3] != head_size:
+            raise ValueError("fp16_k / fp16_v must be [max_seqs, max_ctx, num_kv_heads, head_size]")
+        if t.dtype != torch.float16:
+            raise ValueError("fp16_k / fp16_v must be float16")
+    num_seqs = query.shape[0]
+    max_seqs, max_ctx = fp16_k.shape[:2]
+    if fp16_v.shape[:2] != fp16_k.shape[:2] or num_seqs > max_seqs:
+        raise ValueError("fp16_k / fp16_v shapes disagree or hold fewer sequences than query")
+    page = 16 if max_ctx % 16 == 0 else max_ctx
+    per_seq = max_ctx // page
+    k = fp16_k.contiguous().view(max_seqs * per_seq, page, num_kv_heads, head_size)
+    v = fp16_v.contiguous().view(max_seqs * per_seq, page, num_kv_heads, head_size)
+    block_table = torch.arange(max_seqs * per_seq, dtype=torch.int32,
+                               device=query.device).view(max_seqs, per_seq)[:num_seqs]
+    return fp16_paged_decode(query, k, v, block_table, seq_lens, num_kv_heads, head_size)
+
+
 def decode_kernel_kind(num_heads, num_kv_heads, head_size, k_format, k_group_size, v_format,
                        v_group_size, query_dtype=torch.float16) -> str:
     """'mfma' or 'valu': which decode kernel the library dispatches a shape to."""

@@ -378,3 +378,27 @@ def test_small_magnitude_v_keeps_relative_accuracy(case, sigma):
     out = _run(q, kp, vp, bt, seq_lens, hkv, d)
     ref = A.decode_reference(q.float().numpy(), kp, vp, bt, seq_lens, round_output=False)
     tolerance.check(f"small_v[{name}-{sigma:g}]", out.float().cpu().numpy() / sigma, ref / sigma)
+
+
+@pytest.mark.parametrize("max_ctx", [2048, 1000], ids=["pages_of_16", "one_page_per_sequence"])
+def test_decode_fp16_sdpa_matches_reference_sdpa(max_ctx):
+    """decode_fp16_sdpa (F:2031-2071) on per-sequence fp16 K/V against the
+    reference's own algorithm restated in fp32 on the CPU: per sequence, K/V
+    expanded over the GQA group (repeat_interleave), softmax(q K^T / sqrt(D)) V."""
+    hq, hkv, d = 32, 8, 128
+    seq_lens = [min(1000, max_ctx), 1, 517]
+    ms = 4
+    k = kvgen.randn((ms, max_ctx, hkv, d), 81, outlier_frac=0.01)
+    v = kvgen.randn((ms, max_ctx, hkv, d), 82, outlier_frac=0.01)
+    q = kvgen.randn((len(seq_lens), hq, d), 83)
+    out = K.decode_fp16_sdpa(q.to(DEV), k.to(DEV), v.to(DEV),
+                             torch.tensor(seq_lens, dtype=torch.int32, device=DEV), hkv, hq, d)
+    torch.cuda.synchronize()
+    ref = []
+    for s, n in enumerate(seq_lens):
+        kk = k[s, :n].float().repeat_interleave(hq // hkv, dim=1).transpose(0, 1)   # [H, n, D]
+        vv = v[s, :n].float().repeat_interleave(hq // hkv, dim=1).transpose(0, 1)
+        p = torch.softmax((q[s].float()[:, None, :] @ kk.transpose(1, 2)) * d ** -0.5, dim=-1)
+        ref.append((p @ vv)[:, 0, :])
+    ref = torch.stack(ref).numpy()
+    tolerance.check(f"decode_fp16_sdpa_{max_ctx}", out.float().cpu().numpy(), ref)
