@@ -198,3 +198,46 @@ def test_stream_schedule_workspace_and_limits():
     st = L.knlp_kv_decode_merge(0x100000, ws - 16, 0x60000, 64, 32, 128, 16384, 0,
                                 0x70000, _lib.DT_F16, 32 * 128, 128, None)
     assert st == _lib.ERR_WORKSPACE
+
+
+def test_argument_validation_fuzz_never_crashes():
+    """Random, mostly invalid, shapes, formats, group sizes, strides and
+    pointers through the host-side validation of the plan, workspace, kernel
+    kind and decode entry points.  Decode gets no workspace, so every call
+    returns a status before anything could launch (safe on any machine); the
+    point is that no combination divides by zero or crashes on the host."""
+    import random
+    rng = random.Random(1234)
+    L = _lib.lib()
+    statuses = {0, _lib.ERR_ARG, _lib.ERR_SHAPE, _lib.ERR_DTYPE, _lib.ERR_ALIGN,
+                _lib.ERR_WORKSPACE, _lib.ERR_LAUNCH}
+    pick = rng.choice
+    for _ in range(3000):
+        S = pick([-1, 0, 1, 5, 1025, 70000])
+        hq, hkv = pick([-1, 0, 1, 5, 12, 32, 40]), pick([-1, 0, 1, 4, 8, 12])
+        d = pick([-1, 0, 1, 48, 64, 128, 256, 512])
+        kf, vf = pick([-1, 0, 1, 2, 3, 7]), pick([-1, 0, 1, 2, 3, 7])
+        kgs, vgs = pick([-5, 0, 1, 3, 16, 32, 64, 128, 256]), pick([-5, 0, 1, 3, 32, 64, 128])
+        bs = pick([-1, 0, 1, 15, 16, 17, 32])
+        mc = pick([-1, 0, 1, 100, 32768, (1 << 25) + 1])
+        split = pick([-64, -1, 0, 1, 63, 64, 1024])
+        total = pick([-1, 0, 1, 10 ** 6, 1 << 40])
+        r = L.knlp_kv_decode_plan(S, hkv, hq, d, mc, total, kf, kgs, vf, vgs)
+        assert r >= 0 or r in statuses
+        r = L.knlp_kv_decode_workspace_bytes(S, hq, d, mc, split)
+        assert r >= 0 or r in statuses
+        r = L.knlp_kv_decode_kernel_kind(hq, hkv, d, kf, kgs, vf, vgs, pick([0, 1, 5]))
+        assert r >= 0 or r in statuses
+        kp = _plane(kf, kgs, data=pick([0, 0x1000, 0x1001]), scales=pick([0, 0x2000]),
+                    zeros=pick([0, 0x3000]))
+        vp = _plane(vf, vgs, data=pick([0, 0x4000]), scales=pick([0, 0x5000, 0x5002]),
+                    zeros=pick([0, 0x6000]))
+        for p in (kp, vp):
+            p.stride_head = pick([0, 1, 64, -64, 63])
+            p.s_stride_page = pick([0, 4, 3, 1 << 40])
+        st = L.knlp_kv_decode(pick([0, 0x10000, 0x10002]), pick([0, 1, 5]),
+                              pick([0, 4096, 4095]), pick([0, 128, 127]), S, hq, hkv, d,
+                              ctypes.byref(kp), ctypes.byref(vp), pick([0, 0x50000]),
+                              pick([0, 64]), pick([0, 0x60000]), bs, mc, pick([0.088, -1.0]),
+                              split, None, 0, pick([0, 0x70000]), pick([0, 1]), 4096, 128, None)
+        assert st in statuses and (st != 0 or S == 0), (st, S, hq, hkv, d, kf, vf, kgs, vgs)
