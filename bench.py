@@ -447,8 +447,9 @@ def main(argv=None):
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the decode path is single-GPU in this build "
-              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the decode path is single-GPU in this build (it "
+              "would shard by sequence or kv head, or by pages with the split partials "
+              "all-gathered before the merge); run with --gpus 1", file=sys.stderr)
         return 2
     if args.copy_probe:
         src = torch.ones(args.copy_probe // 4, dtype=torch.float32, device="cuda")
