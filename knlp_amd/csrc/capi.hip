@@ -84,6 +84,13 @@ constexpr int kMaxGridYZ = 65535;
 // lane) and count 32-token tiles in 32 bits (1024 * 2^25 / 32 = 2^30)
 constexpr int kStreamMaxSeqs = 1024;
 constexpr int kStreamMaxContext = 1 << 25;
+// Tiles of work a stream block is charged for each row it starts after its
+// first (the next row's q and block-table loads and the refill of its copy
+// pipeline while the other blocks stream on).  Measured at config 3's shape
+// (64 rows of 512-16384 tokens): a row boundary inside a block costs that
+// block about 7 us, about four 32-token tiles of streaming; charges of 5-8
+// tiles all gave 126.2 us against 129.5 us uncharged, 6 is the middle.
+constexpr int kStreamRowCost = 6;
 
 // A copy of a plane in which an fp16 plane's group_size (a field it does not
 // use: it has no scales) reads head_size, so no later division sees 0.
@@ -345,6 +352,7 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
     a.row_meta = v.meta;
     a.stream_hdr = v.hdr;
     a.stream = P;
+    a.stream_row_cost = kStreamRowCost;
   } else {
     workspace_views(workspace, num_seqs, num_q_heads, head_size, ns, &a.part_o, &a.part_ml);
   }

@@ -48,6 +48,9 @@ struct DecodeArgs {
   // q head] = (its first entry, entry count); stream_hdr[0] = HG, the stride
   // of a q head's entries (read by the merge)
   int stream;               // the block count P of the stream schedule, else 0
+  // tiles of work charged for each row a stream block starts (its first
+  // loads and pipeline fill): shares are equal in tiles + charges
+  int stream_row_cost;
   int32_t* row_meta;
   int32_t* stream_hdr;
   AppendArgs app;

@@ -1328,16 +1328,17 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   return static_cast<uint32_t>(v);
 }
 
-// Where a stream-schedule block starts: the sequence s holding flattened tile
-// f (rows of sequence s are n_s tiles long, nhg rows per sequence, laid end
-// to end in sequence order), its first tile sbase, n_s and its length; and T,
-// all rows' tiles.  The lengths of up to 64 KMAX sequences are loaded at once
-// and scanned 64 at a time; nothing here stays live in the segment loop.
-// Tile counts fit 32 bits: num_seqs * ceil(max_context / 32) < 2^31.
+// Where a stream-schedule block starts: the sequence s holding flattened
+// position f (rows of sequence s are cost + n_s positions long, nhg rows per
+// sequence, laid end to end in sequence order), its first position sbase,
+// n_s and its length; and T, all rows' positions.  The lengths of up to 64
+// KMAX sequences are loaded at once and scanned 64 at a time; nothing here
+// stays live in the segment loop.  Position counts fit 32 bits:
+// num_seqs * (ceil(max_context / 32) + cost) < 2^31.
 struct StreamStart {
   static constexpr int KMAX = 16;    // up to 1024 sequences
   uint64_t T, sbase;
-  uint32_t n;
+  uint32_t n, cost;
   int s, len, Pe;
 
   __device__ __forceinline__ void find(const DecodeArgs& a, int nhg, int b, int P, int lane,
@@ -1349,13 +1350,29 @@ struct StreamStart {
       const int i = kWave * k + lane;
       len_k[k] = (k < nk && i < a.num_seqs) ? a.seq_lens[i] : 0;
     }
+    // all rows' tiles (nhg rows per sequence)
+    uint64_t tiles = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k)
+      if (k < nk)                                             // uniform
+        tiles += static_cast<uint32_t>(__builtin_amdgcn_readlane(
+            static_cast<int>(wave_incl_scan(seq_tiles(len_k[k], a.max_context))), 63));
+    // Each row after a block's first costs the block its first loads and a
+    // refill of its copy pipeline: a row is laid out as `cost` charged
+    // positions then its n tiles, and blocks take equal shares of positions.
+    // Charged only when every block's share exceeds `cost` positions (so every
+    // block holds a tile, and holds no row's charged positions alone).
+    cost = static_cast<uint64_t>(nhg) * tiles >= static_cast<uint64_t>(a.stream_row_cost + 1) * P
+               ? static_cast<uint32_t>(a.stream_row_cost) : 0u;
+    // inclusive prefix sums of the sequences' positions
     uint32_t incl[KMAX];
     uint64_t total = 0;
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
       incl[k] = 0;
-      if (k < nk) {                                           // uniform
-        incl[k] = wave_incl_scan(seq_tiles(len_k[k], a.max_context));
+      if (k < nk) {
+        const uint32_t t = seq_tiles(len_k[k], a.max_context);
+        incl[k] = wave_incl_scan(t > 0 ? t + cost : 0u);
         total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[k]), 63));
       }
     }
@@ -1396,7 +1413,8 @@ struct StreamStart {
     n = seq_tiles(len, a.max_context);
     if (s >= a.num_seqs || n == 0) return;                    // (cannot happen either)
     sbase = static_cast<uint64_t>(nhg) *
-            (acc + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ik), c)) - n);
+            (acc + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ik), c)) -
+             (n + cost));
     *f0 = f;
     *f1 = static_cast<uint64_t>(b + 1) * T / Pe;
   }
@@ -1408,14 +1426,16 @@ struct StreamStart {
 //
 // Schedules.  Split (a.stream == 0): block (split, seq, head group) runs the
 // tokens [split * split_tokens, ...) of one sequence.  Stream (a.stream = P):
-// the grid is one block per CU, and block b < Pe = min(P, T) runs the tiles
-// [b T / Pe, (b + 1) T / Pe) of all (sequence, head group) rows laid end to
-// end (T tiles of 32 tokens in all): equal work per block whatever the
-// sequence lengths, one partial per (block, row) segment, at entry
-// (b + row) * HG + head, a number no two segments share (b + row is strictly
-// increasing along the flattened tiles).  The block holding a row's first
-// tile writes, for each q head of the row, its first entry and the count of
-// blocks holding the row for the merge.
+// the grid is one block per CU, and block b < Pe = min(P, T) runs the
+// positions [b T / Pe, (b + 1) T / Pe) of all (sequence, head group) rows laid
+// end to end, each row a charge of `cost` positions (no work: what starting
+// a row costs a block) then its tiles of 32 tokens (T positions in all):
+// equal work per block whatever the sequence lengths, one partial per
+// (block, row) segment, at entry (b + row) * HG + head, a number no two
+// segments share (b + row is strictly increasing along the flattened rows).
+// The block holding a row's first tile writes, for each q head of the row,
+// its first entry and the count of blocks holding the row's tiles for the
+// merge.
 
 // One segment: tokens [t_begin, t_begin + seg_tokens) (cut at the sequence's
 // length) of sequence `seq`, kv heads 8 hg .. 8 hg + 7.  seq_len < 0: load it
@@ -1566,31 +1586,31 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
   }
 }
 
-// The stream schedule's walk over the flattened tiles: the next tile f, the
-// block's end fe, all tiles T, the current sequence s (its rows start at
-// tile sbase and are n tiles long; len tokens) and the blocks taking part
-// Pe.  Through each segment's tile loop it lives in the lanes of one VGPR
+// The stream schedule's walk over the flattened positions: the next position
+// f, the block's end fe, all positions T, the current sequence s (its rows
+// start at position sbase and are cost + n positions long, the charge then n
+// tiles; len tokens) and the blocks taking part Pe.  Through each segment's tile loop it lives in the lanes of one VGPR
 // (hold() returns it, field i in lane i): as uniform values the compiler would keep
 // its 12 words in SGPRs, which the tile loop needs all of, or in 12 VGPRs,
 // which a two-head-set tile loop does not have to spare; uniform() reads it
 // back at segment boundaries.
 struct StreamWalk {
   uint64_t f, fe, T, sbase;
-  uint32_t n;
+  uint32_t n, cost;
   int s, len, Pe;
 
   // the walk in one VGPR, field i in lane i
   __device__ __forceinline__ uint32_t hold() const {
-    const uint32_t w[12] = {static_cast<uint32_t>(f),     static_cast<uint32_t>(f >> 32),
+    const uint32_t w[13] = {static_cast<uint32_t>(f),     static_cast<uint32_t>(f >> 32),
                             static_cast<uint32_t>(fe),    static_cast<uint32_t>(fe >> 32),
                             static_cast<uint32_t>(T),     static_cast<uint32_t>(T >> 32),
                             static_cast<uint32_t>(sbase), static_cast<uint32_t>(sbase >> 32),
                             n, static_cast<uint32_t>(s), static_cast<uint32_t>(len),
-                            static_cast<uint32_t>(Pe)};
+                            static_cast<uint32_t>(Pe), cost};
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     uint32_t v = 0;
 #pragma unroll
-    for (int i = 0; i < 12; ++i) v = lane == i ? w[i] : v;
+    for (int i = 0; i < 13; ++i) v = lane == i ? w[i] : v;
     asm volatile("" : "+v"(v));     // opaque: reads below come from the VGPR
     return v;
   }
@@ -1608,6 +1628,7 @@ struct StreamWalk {
     u.s = static_cast<int>(lane(9));
     u.len = static_cast<int>(lane(10));
     u.Pe = static_cast<int>(lane(11));
+    u.cost = lane(12);
     return u;
   }
 };
@@ -1651,6 +1672,7 @@ __device__ __forceinline__ void coop_kernel_body(
       W.s = st.s;
       W.len = st.len;
       W.Pe = st.Pe;
+      W.cost = st.cost;
       walk = W.hold();
     }
     while (true) {                                            // uniform
@@ -1658,18 +1680,23 @@ __device__ __forceinline__ void coop_kernel_body(
       const StreamWalk U = StreamWalk::uniform(walk);
       const int nhg = a.num_kv_heads / L::kHeads;
       const int HG = L::kHeads * a.group;
-      const int hg = static_cast<int>((U.f - U.sbase) / U.n);
+      const uint32_t nv = U.n + U.cost;                     // a row's positions
+      const int hg = static_cast<int>((U.f - U.sbase) / nv);
       if (hg >= nhg) break;                                   // (cannot happen)
-      const uint64_t srow = U.sbase + static_cast<uint64_t>(hg) * U.n;
-      const uint64_t send = min(U.fe, srow + U.n);
-      const int t0 = static_cast<int>(U.f - srow);
-      const int t1 = static_cast<int>(send - srow);
+      const uint64_t srow = U.sbase + static_cast<uint64_t>(hg) * nv;
+      const uint64_t r0 = srow + U.cost;                      // the row's first tile
+      const uint64_t send = min(U.fe, srow + nv);
+      // the block's share ends among the row's charged positions: no tile of
+      // it here (the next block starts the row)
+      if (send <= r0) break;
+      const int t0 = static_cast<int>(max(U.f, r0) - r0);
+      const int t1 = static_cast<int>(send - r0);
       const int row = U.s * nhg + hg;
       if (t0 == 0 && static_cast<int>(threadIdx.x) < HG) {
         // the row's record, one per q head j: its first entry and the count
-        // of blocks holding the row's tiles (the block holding flattened tile
-        // t: the b with floor(b T / Pe) <= t < floor((b + 1) T / Pe))
-        const uint64_t tl = srow + U.n - 1;
+        // of blocks holding the row's tiles (the block holding flattened
+        // position t: the b with floor(b T / Pe) <= t < floor((b + 1) T / Pe))
+        const uint64_t tl = srow + nv - 1;
         const int j = threadIdx.x;
         int32_t* rec = a.row_meta + 2 * (static_cast<int64_t>(U.s) * a.num_q_heads + hg * HG + j);
         rec[0] = (b + row) * HG + j;
@@ -1696,7 +1723,7 @@ __device__ __forceinline__ void coop_kernel_body(
       __syncthreads();    // the next segment's copies reuse the tile buffers
       // past this sequence's rows: the next sequence with tiles (one exists,
       // since tiles remain before fe <= T)
-      if (V.f == V.sbase + static_cast<uint64_t>(nhg) * V.n) {
+      if (V.f == V.sbase + static_cast<uint64_t>(nhg) * (V.n + V.cost)) {
         V.sbase = V.f;
         V.n = 0;
         while (V.n == 0 && V.s + 1 < a.num_seqs) {

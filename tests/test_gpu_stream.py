@@ -8,7 +8,8 @@ bar (tests/tolerance.py) and against the split schedule on the same inputs.
 Edge cases: zero-length sequences (NaN like the reference's 0/0, F:886-887),
 lengths 1, 31, 32, 33 around the tile, batches with fewer tiles than blocks
 (most blocks idle), one sequence spread over every block, several hundred
-sequences (the in-kernel length scan spans several wave passes), two head sets,
+sequences (the in-kernel length scan spans several wave passes), batches
+large enough that row starts are charged to the blocks, two head sets,
 INT8 K and V, D = 64, bf16 q; planes the cooperative kernel does not take
 (split-K inside the stream workspace) and the sequence limit."""
 import numpy as np
@@ -46,6 +47,14 @@ CASES = [
     ("int4_g6_two_sets", [1, 16, 47, 900], 48, 8, 128, 0, 0, 32, 32),
     ("many_sequences_300", _lens(300, 0, 200, 1, zeros=5), 32, 8, 128, 1, 1, 32, 32),
     ("max_sequences_1024", _lens(1024, 1, 40, 2), 32, 8, 128, 1, 1, 32, 32),
+    # more than 5 tiles per block (256 CUs): each row a block starts after its
+    # first is charged to it, so shares are unequal in tiles; rows shorter
+    # than the charge, empty sequences, two rows per sequence
+    ("charged_rows", _lens(48, 1, 3000, 3, zeros=3), 32, 8, 128, 1, 1, 32, 32),
+    ("charged_short_and_long_rows", _lens(200, 1, 100, 5) + [30000, 20000, 1], 32, 8, 128, 1,
+     1, 32, 32),
+    ("charged_two_rows_per_seq", _lens(24, 1, 3000, 4), 64, 16, 128, 1, 1, 32, 32),
+    ("charged_kint8_row_two_sets", _lens(30, 1, 3000, 6, zeros=2), 40, 8, 128, 2, 1, 128, 32),
 ]
 
 
@@ -107,8 +116,10 @@ def test_stream_schedule_sequence_limit():
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("seq_lens", [[1, 17, 31, 32, 33, 0, 511, 2049, 700], [3000, 2, 0, 90]],
-                         ids=["fewer_tiles_than_blocks", "more_tiles_than_blocks"])
+@pytest.mark.parametrize("seq_lens", [[1, 17, 31, 32, 33, 0, 511, 2049, 700], [3000, 2, 0, 90],
+                                      _lens(40, 0, 3000, 6, zeros=4)],
+                         ids=["fewer_tiles_than_blocks", "more_tiles_than_blocks",
+                              "charged_rows"])
 def test_stream_schedule_reads_only_what_it_wrote(seq_lens):
     """The workspace filled with NaN before the call: every partial the merge
     reads was written by this launch (a stale or unwritten entry would
