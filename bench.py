@@ -662,7 +662,7 @@ def main(argv=None):
                    "head_dim": D, "context": int(np.max(seq_lens)),
                    "total_tokens": int(np.sum(seq_lens)), "block_size": bs,
                    "split_tokens": split, "split_tokens_planned": split_plan,
-                   "schedule": "stream (one workgroup per CU, equal tile shares)"
+                   "schedule": "stream (one workgroup per CU, equal shares of tiles + row charges)"
                                if split == 0 else "split-K",
                    "split_sweep_us_per_step": {str(k): round(v * 1e3, 2)
                                                for k, v in split_tried.items()},
