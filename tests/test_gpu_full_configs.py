@@ -5,8 +5,9 @@ the checks are the size-independent properties the reference's own at-shape
 validation relies on (scripts/v35_h100_bench.py:634-688), plus an oracle
 comparison on one sampled (sequence, kv head):
 
-* the library's split plan and two other split lengths agree within the bar
-  (split-count invariance: the same attention, other summation orders);
+* the library's plan (split-K, or the stream schedule at config 3) and other
+  split lengths, and the stream schedule, agree within the bar (split-count
+  invariance: the same attention, other summation orders);
 * two runs are bit-identical (determinism);
 * every output is finite;
 * a physical permutation of the pages with the block table permuted to
@@ -129,10 +130,13 @@ def _decode(cfg, q, kp, vp, bt_d, sl, split=None):
     return out
 
 
-def _plan(cfg, bt_d, kp, vp):
+def _plan(cfg, bt_d, lens):
+    """The library's plan with the batch's total context known on the host (as
+    the vLLM backend passes it): split-K for the uniform configurations, the
+    stream schedule (0) for config 3's variable lengths."""
     return _lib.lib().knlp_kv_decode_plan(cfg["B"], cfg["Hkv"], cfg["Hq"], D,
-                                          bt_d.shape[1] * BS, 0, FMT[cfg["k"]], cfg["kgs"],
-                                          FMT[cfg["v"]], cfg["vgs"])
+                                          bt_d.shape[1] * BS, int(np.sum(lens)), FMT[cfg["k"]],
+                                          cfg["kgs"], FMT[cfg["v"]], cfg["vgs"])
 
 
 def _sampled_oracle(c, cfg, q, kp, vp, bt, lens, out):
@@ -157,14 +161,16 @@ def test_full_size_config(c):
     kind = K.decode_kernel_kind(cfg["Hq"], cfg["Hkv"], D, FMT[cfg["k"]], cfg["kgs"],
                                 FMT[cfg["v"]], cfg["vgs"])
     assert kind == "mfma"
-    plan = _plan(cfg, bt_d, kp, vp)
-    print(f"config {c}: plan {plan} tokens per split", flush=True)
+    plan = _plan(cfg, bt_d, lens)
+    print(f"config {c}: plan {plan} tokens per split (0: stream schedule)", flush=True)
+    assert (plan == 0) == (c == 3)
     out = _decode(cfg, q, kp, vp, bt_d, sl, plan)
     assert torch.isfinite(out.float()).all()
     again = _decode(cfg, q, kp, vp, bt_d, sl, plan)
     assert torch.equal(out.view(torch.int16), again.view(torch.int16)), "not deterministic"
     got = out.float().cpu().numpy()
-    for other in sorted({max(64, plan // 2 // 64 * 64), plan * 2, 1024} - {plan}):
+    others = {1024, 2048} if plan == 0 else {max(64, plan // 2 // 64 * 64), plan * 2, 1024, 0}
+    for other in sorted(others - {plan}):
         o2 = _decode(cfg, q, kp, vp, bt_d, sl, other).float().cpu().numpy()
         tolerance.check(f"full_config{c}_split{other}_vs_plan{plan}", o2, got)
     _sampled_oracle(c, cfg, q, kp, vp, bt, lens, out)

@@ -169,3 +169,84 @@ def test_stream_schedule_all_sequences_empty():
     q = _query(3, 32, 128, 75)
     out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=0)
     assert torch.isnan(out.float()).all()
+
+
+def _random_pages(lens, hq, hkv, d, kint8, seed):
+    """A paged batch with random codes and scales generated on the device (any
+    byte is a valid code): sizes beyond what the oracle decodes in a test."""
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    bs = 16
+    pages = [-(-int(n) // bs) for n in lens]
+    nb = sum(pages) + 5
+    width = max(max(pages), 1)
+    perm = torch.randperm(nb, generator=g, device=DEV).to(torch.int32)
+    bt = torch.zeros(len(lens), width, dtype=torch.int32, device=DEV)
+    cur = 0
+    for s, p in enumerate(pages):
+        bt[s, :p] = perm[cur:cur + p]
+        cur += p
+
+    def scales(ng):
+        return (0.05 + 0.15 * torch.rand(nb, bs, hkv, ng, generator=g, device=DEV)).half()
+
+    # the planes hold raw pointers: every tensor stays referenced in `keep`
+    if kint8:
+        kd = torch.randint(-127, 128, (nb, bs, hkv, d), generator=g, device=DEV).to(torch.int8)
+        ks, kz = scales(1), None
+        kp = ops._plane(kd, ks, kz, 2, d)
+    else:
+        kd = torch.randint(0, 256, (nb, bs, hkv, d // 2), generator=g, device=DEV).to(torch.uint8)
+        ks = scales(d // 32)
+        kz = (-8 * ks.float()).half()
+        kp = ops._plane(kd, ks, kz, 1, 32)
+    vd = torch.randint(0, 256, (nb, bs, hkv, d // 2), generator=g, device=DEV).to(torch.uint8)
+    vs = scales(d // 32)
+    vz = (-8 * vs.float()).half()
+    vp = ops._plane(vd, vs, vz, 1, 32)
+    q = torch.randn(len(lens), hq, d, generator=g, device=DEV).half()
+    keep = (kd, ks, kz, vd, vs, vz)
+    return q, kp, vp, bt, torch.tensor(lens, dtype=torch.int32, device=DEV), keep
+
+
+@pytest.mark.parametrize("trial", range(12))
+def test_stream_matches_split_on_random_batches(trial):
+    """Random batches of 1-700 sequences with lengths from three mixes
+    (uniform up to 12000 tokens; extremes 0/1/31/33/100/4000/12000; heavy
+    tailed), one or two kv-head groups, INT4 or INT8 K: the stream schedule,
+    with or without row charges (depending on the batch's size), gives what
+    split-K gives, to the bar, and the same bits twice.  A tile dropped or
+    taken twice by a block's share, or a partial merged from a wrong entry,
+    shows up as a difference."""
+    g = np.random.default_rng(500 + trial)
+    S = int(g.choice([1, 3, 17, 64, 200, 700]))
+    mix = trial % 3
+    if mix == 0:
+        lens = g.integers(0, 12001, S)
+    elif mix == 1:
+        lens = g.choice([0, 1, 31, 33, 100, 4000, 12000], S)
+    else:
+        lens = np.minimum((g.pareto(1.2, S) * 300).astype(np.int64), 12000)
+    lens = [int(x) for x in lens]
+    while sum(lens) > 2_000_000:                   # bound the pool at about 2 GB
+        lens = lens[: len(lens) // 2]
+    hkv = 16 if trial % 4 == 3 else 8
+    kint8 = trial % 5 == 4
+    hq = (5 if kint8 else 4) * hkv
+    tiles = sum(-(-n // 32) for n in lens) * (hkv // 8)
+    print(f"random batch {trial}: {len(lens)} sequences, {sum(lens)} tokens, {tiles} row "
+          f"tiles, hkv {hkv}, k {'int8' if kint8 else 'int4'}", flush=True)
+    q, kp, vp, bt, sl, keep = _random_pages(lens, hq, hkv, 128, kint8, 900 + trial)
+
+    def run(split):
+        out = ops._decode(q, kp, vp, 16, bt, sl, hkv, 128, split_tokens=split)
+        torch.cuda.synchronize()
+        return out
+
+    stream = run(0)
+    split = run(512)
+    valid = np.array([n > 0 for n in lens])
+    tolerance.check(f"stream_random_{trial}_vs_split512", stream.float().cpu().numpy()[valid],
+                    split.float().cpu().numpy()[valid])
+    assert torch.isnan(stream.float().cpu()[~torch.from_numpy(valid)]).all()
+    assert torch.equal(stream.view(torch.int16), run(0).view(torch.int16)), "not deterministic"
+    del keep
