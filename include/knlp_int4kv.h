@@ -127,8 +127,9 @@ int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads,
  * Stream schedule (split_tokens = 0 in the calls below): one workgroup per
  * CU, each taking an equal share of all (sequence, group of 8 kv heads)
  * rows' 32-token tiles laid end to end, so sequences of any mix of lengths
- * keep every CU busy to the end; the merge folds each row's per-workgroup
- * partials.  Its workspace depends on num_seqs, not max_context.  Planes the
+ * keep every CU busy to the end (in large batches each row a workgroup
+ * starts after its first counts as 6 tiles of its share: the row's start-up
+ * costs about that); the merge folds each row's per-workgroup partials.  Its workspace depends on num_seqs, not max_context.  Planes the
  * cooperative kernel cannot take (fp16 K, Hkv % 8 != 0, a sparse layout)
  * run split-K inside that workspace instead.  More than 1024 sequences or
  * max_context > 2^25 with split_tokens = 0 is KNLP_ERR_SHAPE.
