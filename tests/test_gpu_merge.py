@@ -1,0 +1,45 @@
+"""The merge's two kernels and its fold's group sizes, against the oracle.
+
+The merge folds each (sequence, q head)'s partials in groups of 8, then one
+group of 4, 2 and 1 (every load in a group is of a real partial), either with
+one wave per head (merge_wave_kernel: at most 2 partials, or at most 16 with
+more than 2048 heads in the batch) or four to sixteen waves per head
+(merge_kernel, waves taking every 4th partial).  64-token splits over lengths
+0-1024 give every partial count from 0 to 16 in one batch, so every tail of
+the fold runs; empty sequences must give NaN (0/0, F:886-887).  Checked
+against the oracle's dequantise -> SDPA (scripts/v35_h100_bench.py:376-387)
+to the shared bar (tests/tolerance.py)."""
+import numpy as np
+import pytest
+
+from tests.test_gpu_decode import _build, _check, _query, _run
+
+pytestmark = pytest.mark.gpu
+
+
+def _lens(n, lo, hi, seed, zeros=()):
+    g = np.random.default_rng(seed)
+    out = g.integers(lo, hi + 1, n).tolist()
+    for i in zeros:
+        out[i] = 0
+    return out
+
+
+@pytest.mark.parametrize("case", [
+    # name, seq_lens, hq, split: one wave per head (80 x 32 heads > 2048), 0-16 partials
+    ("wave_kernel_all_counts", _lens(80, 1, 1024, 11, zeros=(3, 40)) + list(range(1, 1025, 64)),
+     32, 64),
+    # one wave per head (at most 2 partials) with few heads
+    ("wave_kernel_few_heads", [1, 64, 65, 128, 0, 100], 32, 64),
+    # four waves per head (8 x 32 heads), 5-16 partials: every tail at step 4
+    ("four_waves_tails", [300, 400, 449, 513, 640, 705, 900, 1024], 32, 64),
+    # sixteen waves per head: 80 partials
+    ("sixteen_waves", [5100, 77], 32, 64),
+], ids=lambda c: c[0])
+def test_merge_kernels_and_fold_tails(case):
+    name, seq_lens, hq, split = case
+    print(f"merge case {name}: {len(seq_lens)} sequences, split {split}", flush=True)
+    bt, kp, vp = _build(seq_lens, hq, 8, 128, 1, 1, 32, 32, seed=80)
+    q = _query(len(seq_lens), hq, 128, 80)
+    out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=split)
+    _check(out, q, kp, vp, bt, seq_lens, name=f"merge_{name}")
