@@ -97,8 +97,8 @@ int knlp_kv_append(const void* key, const void* value, int32_t src_dtype,
                    int32_t block_size, float clip_ratio, void* stream);
 
 /*
- * Split-K plan: tokens per split for a batch whose longest possible context
- * is max_context (= block-table width * block_size; no device read-back),
+ * Split-K plan: tokens per split for a batch of num_seqs sequences taken at
+ * max_context each (= block-table width * block_size; no device read-back),
  * for K/V planes of the given knlp_kv_format values, taking one scale per
  * row for INT8 planes and group size 32 for INT4 planes (the reference's
  * default GROUP_SIZE, F:55); knlp_kv_decode_plan takes the group sizes and
@@ -116,12 +116,15 @@ int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads,
  * total_context -- the sum of the batch's sequence lengths, when the caller
  * knows it on the host (vLLM's metadata does) -- sizes the splits of a
  * variable-length batch from its real work; total_context <= 0 means
- * unknown (every sequence taken at max_context).  Returns the split length
- * in tokens (> 0, a multiple of 64), 0 for the stream schedule (below), or
- * a negative status.  0 is returned for variable-length batches (total
- * context at most 90 % of num_seqs * max_context) that the cooperative
- * matrix-core kernel takes (Hkv % 8 == 0, INT4/INT8 K, at most 1024
- * sequences, max_context <= 2^25).  No counterpart in the reference (it has
+ * unknown.  Returns the split length in tokens (> 0, a multiple of 64), 0
+ * for the stream schedule (below), or a negative status.  0 is returned,
+ * when the cooperative matrix-core kernel takes the planes (Hkv % 8 == 0,
+ * INT4/INT8 K, at most 1024 sequences, max_context <= 2^25), for
+ * variable-length batches (total context at most 90 % of num_seqs *
+ * max_context) and for batches of several sequences whose total is unknown
+ * (the stream schedule's equal shares hold for any mix of lengths; splits
+ * sized for every sequence at max_context leave a long sequence among short
+ * ones to a few workgroups).  No counterpart in the reference (it has
  * no split-K).
  *
  * Stream schedule (split_tokens = 0 in the calls below): one workgroup per

@@ -213,13 +213,19 @@ int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads, int32_t num_
   // rows run more splits than the grid's last round holds), so the
   // cooperative kernel's stream schedule (0) deals all rows' tiles out in
   // equal shares instead (config 3: 180 -> 130 us).  Uniform batches keep
-  // split-K, whose start-up is about 2 us shorter.
+  // split-K, whose start-up is about 2 us shorter.  With the total unknown
+  // and several sequences the stream schedule runs too: its shares hold for
+  // any mix of lengths, while splits sized for every sequence at max_context
+  // leave a long sequence among short ones to a few workgroups (one
+  // 100000-token sequence among 127 of 500 tokens: 1869 us per step against
+  // 44 us).
   // (Two head sets with fewer than 4 V groups run out of registers in the
   // stream kernel and stay on split-K.)
   const int vng = v_format == KNLP_KV_FP16 || v_group_size <= 0 ? 1 : head_size / v_group_size;
   const bool stream_fits = g * vng <= 16 || vng == 4;
-  if (wide && stream_fits && total_context > 0 && 10 * total <= 9 * rect &&
-      num_seqs <= kStreamMaxSeqs && max_context <= kStreamMaxContext)
+  const bool ragged = total_context > 0 ? 10 * total <= 9 * rect : num_seqs > 1;
+  if (wide && stream_fits && ragged && num_seqs <= kStreamMaxSeqs &&
+      max_context <= kStreamMaxContext)
     return 0;
   int64_t tok = (total * hgroups + target - 1) / target;
   if (tok < 64) tok = 64;
@@ -235,8 +241,10 @@ int32_t knlp_kv_decode_split_tokens(int32_t num_seqs, int32_t num_kv_heads, int3
   // 32 (the reference's default GROUP_SIZE, F:55) for INT4
   const auto gs = [&](int f) { return f == KNLP_KV_INT8_SYM ? head_size : 32; };
   if (num_q_heads <= 0) num_q_heads = num_kv_heads;
-  return knlp_kv_decode_plan(num_seqs, num_kv_heads, num_q_heads, head_size, max_context, 0,
-                             k_format, gs(k_format), v_format, gs(v_format));
+  // a split length: the batch taken as uniform (every sequence at max_context)
+  return knlp_kv_decode_plan(num_seqs, num_kv_heads, num_q_heads, head_size, max_context,
+                             static_cast<int64_t>(num_seqs) * max_context, k_format,
+                             gs(k_format), v_format, gs(v_format));
 }
 
 int64_t knlp_kv_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t head_size,

@@ -19,8 +19,10 @@ reference's behaviour:
   * ``split_tokens`` -- split-K length, default from the library's plan; 0 is
     the stream schedule (equal shares of all rows' tiles per CU);
   * ``total_context`` -- the batch's summed sequence lengths when the caller
-    knows them on the host (0: unknown); the plan picks the stream schedule
-    for variable-length batches from it.
+    knows them on the host (0: unknown); with it the plan keeps split-K for
+    uniform batches and picks the stream schedule for variable-length ones;
+    unknown, it picks the stream schedule for any batch of several sequences
+    the cooperative kernel takes.
 ``block_n`` is accepted for signature compatibility and ignored: the HIP
 kernels pick their own token tiles.
 """

@@ -156,8 +156,11 @@ def test_decode_plan_uses_group_sizes_and_total_context():
     L = _lib.lib()
     a4, i8 = _lib.KV_INT4_ASYM, _lib.KV_INT8_SYM
     legacy = L.knlp_kv_decode_split_tokens(8, 8, 32, 128, 32768, a4, a4)
-    assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, a4, 32, a4, 32) == legacy
+    assert legacy > 0                                       # always a split length
     assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 8 * 32768, a4, 32, a4, 32) == legacy
+    # the total unknown: the stream schedule for several sequences, a split for one
+    assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, a4, 32, a4, 32) == 0
+    assert L.knlp_kv_decode_plan(1, 8, 32, 128, 32768, 0, a4, 32, a4, 32) > 0
     # a variable-length batch (half the tokens of its rectangle) on the
     # cooperative kernel: the stream schedule (0)
     assert L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 64 * 8192, a4, 32, a4, 32) == 0
@@ -170,8 +173,8 @@ def test_decode_plan_uses_group_sizes_and_total_context():
     assert 64 <= var < full and var % 64 == 0
     # INT8 V with g64 runs on the VALU kernel (two workgroups per CU): half
     # the split length of the cooperative kernel's plan for the same shape
-    coop = L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, i8, 128, i8, 128)
-    valu = L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 0, i8, 128, i8, 64)
+    coop = L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 8 * 32768, i8, 128, i8, 128)
+    valu = L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 8 * 32768, i8, 128, i8, 64)
     assert valu < coop
     assert L.knlp_kv_decode_plan(8, 7, 32, 128, 32768, 0, a4, 32, a4, 32) == _lib.ERR_SHAPE
 
