@@ -106,18 +106,23 @@ int check_head_size(int head_size) {
              : KNLP_ERR_SHAPE;
 }
 
+// CUs of the first device asked (every MI355X has 256); the stream
+// schedule's grid and workspace size use it.  Threads racing on the first
+// call store the same value.
 int num_cus() {
-  static int cached = 0;
-  if (cached == 0) {
+  static std::atomic<int> cached{0};
+  int c = cached.load(std::memory_order_relaxed);
+  if (c == 0) {
     int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        n > 0)
-      cached = n;
-    else
-      cached = 256;   // MI355X
+    c = hipGetDevice(&dev) == hipSuccess &&
+                hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                    hipSuccess &&
+                n > 0
+            ? n
+            : 256;   // MI355X
+    cached.store(c, std::memory_order_relaxed);
   }
-  return cached;
+  return c;
 }
 
 int heads_per_block(int num_kv_heads) {
