@@ -20,8 +20,8 @@ RTOL_F16 = 2.0 ** -10
 RTOL_BF16 = 2.0 ** -8
 
 # (case, max-abs error where |ref| <= 2, max error / bar over all elements,
-#  max-abs error over all elements, max |ref|)
-RESULTS: list[tuple[str, float, float, float, float]] = []
+#  max-abs error over all elements, max |ref|, bf16 output)
+RESULTS: list[tuple[str, float, float, float, float, bool]] = []
 
 
 def bound(ref: np.ndarray, bf16: bool = False) -> np.ndarray:
@@ -43,7 +43,7 @@ def check(name: str, got: np.ndarray, ref: np.ndarray, bf16: bool = False) -> fl
     small = np.abs(ref) <= F16_KNEE
     RESULTS.append((name, float(err[small].max()) if small.any() else 0.0,
                     float((err / b).max()) if err.size else 0.0, m,
-                    float(np.abs(ref).max()) if ref.size else 0.0))
+                    float(np.abs(ref).max()) if ref.size else 0.0, bf16))
     over = err > b
     assert not over.any(), (f"{name}: max abs err {m:.3e}; {int(over.sum())} elements over "
                             f"the bar, worst at |ref| = {float(np.abs(ref)[over].max()):.3g}")
