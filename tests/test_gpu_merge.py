@@ -26,20 +26,23 @@ def _lens(n, lo, hi, seed, zeros=()):
 
 
 @pytest.mark.parametrize("case", [
-    # name, seq_lens, hq, split: one wave per head (80 x 32 heads > 2048), 0-16 partials
+    # name, seq_lens, hq, d, split: one wave per head (80 x 32 heads > 2048), 0-16 partials
     ("wave_kernel_all_counts", _lens(80, 1, 1024, 11, zeros=(3, 40)) + list(range(1, 1025, 64)),
-     32, 64),
-    # one wave per head (at most 2 partials) with few heads
-    ("wave_kernel_few_heads", [1, 64, 65, 128, 0, 100], 32, 64),
+     32, 128, 64),
+    # one wave per head (at most 2 partials) with few heads; D = 64 and 256 (1 and 4
+    # elements per lane)
+    ("wave_kernel_few_heads", [1, 64, 65, 128, 0, 100], 32, 128, 64),
+    ("wave_kernel_d64", [1, 64, 100, 0, 128], 16, 64, 64),
+    ("wave_kernel_d256", [1, 64, 100, 128], 64, 256, 64),
     # four waves per head (8 x 32 heads), 5-16 partials: every tail at step 4
-    ("four_waves_tails", [300, 400, 449, 513, 640, 705, 900, 1024], 32, 64),
+    ("four_waves_tails", [300, 400, 449, 513, 640, 705, 900, 1024], 32, 128, 64),
     # sixteen waves per head: 80 partials
-    ("sixteen_waves", [5100, 77], 32, 64),
+    ("sixteen_waves", [5100, 77], 32, 128, 64),
 ], ids=lambda c: c[0])
 def test_merge_kernels_and_fold_tails(case):
-    name, seq_lens, hq, split = case
-    print(f"merge case {name}: {len(seq_lens)} sequences, split {split}", flush=True)
-    bt, kp, vp = _build(seq_lens, hq, 8, 128, 1, 1, 32, 32, seed=80)
-    q = _query(len(seq_lens), hq, 128, 80)
-    out = _run(q, kp, vp, bt, seq_lens, 8, 128, split_tokens=split)
+    name, seq_lens, hq, d, split = case
+    print(f"merge case {name}: {len(seq_lens)} sequences, d {d}, split {split}", flush=True)
+    bt, kp, vp = _build(seq_lens, hq, 8, d, 1, 1, 32, 32, seed=80)
+    q = _query(len(seq_lens), hq, d, 80)
+    out = _run(q, kp, vp, bt, seq_lens, 8, d, split_tokens=split)
     _check(out, q, kp, vp, bt, seq_lens, name=f"merge_{name}")
