@@ -1123,7 +1123,14 @@ struct CoopAddr {
 };
 
 // 16 bytes per lane from global memory (64-bit scalar base + 32-bit lane
-// offset) straight into LDS at m0 + 16 * lane.
+// offset) straight into LDS at m0 + 16 * lane, non-temporal (gfx950 cache
+// policy NT): each K/V byte is read once per launch, in whole lines, by the
+// one workgroup that copies its page, so the lines need not stay in the
+// caches.  At config 2 the partial went from 65.6 to 59.4 us with the hint
+// (and a plain streaming read of the same bytes from 0.764 to 0.811 of
+// 8 TB/s).  The per-head and VALU kernels keep default loads: their waves
+// read one head's slice of lines that neighbouring heads' waves read too
+// (with the hint their fp16 decode at config 3 took 724 us against 519).
 // Written as inline asm so that the compiler does not track these copies:
 // its conservative tracking would put a full vector-memory wait before
 // every LDS read, serialising the copies of later tiles with the compute of
@@ -1142,7 +1149,7 @@ __device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, cons
   // null check
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_dst)));
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                :
                : "v"(voff), "s"(sb), "s"(m0)
                : "memory", "m0");

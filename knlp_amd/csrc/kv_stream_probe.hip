@@ -12,6 +12,8 @@
 
 namespace knlp {
 
+using vu4 = unsigned int __attribute__((ext_vector_type(4)));
+
 template <int NLOAD>
 __global__ __launch_bounds__(512) void hbm_read_kernel(const uint4* __restrict__ src, int64_t n16,
                                                        int64_t per_block,
@@ -25,7 +27,13 @@ __global__ __launch_bounds__(512) void hbm_read_kernel(const uint4* __restrict__
 #pragma unroll
     for (int k = 0; k < NLOAD; ++k) {
       const int64_t j = i + static_cast<int64_t>(k) * blockDim.x;
-      v[k] = j < end ? src[j] : make_uint4(0, 0, 0, 0);
+      if (j < end) {
+        // non-temporal, like the decode kernel's tile copies: streamed once
+        const vu4 w = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(src) + j);
+        v[k] = make_uint4(w.x, w.y, w.z, w.w);
+      } else {
+        v[k] = make_uint4(0, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int k = 0; k < NLOAD; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
