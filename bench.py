@@ -614,7 +614,11 @@ def main(argv=None):
                  "fp16_step_GBs": round(alg16 / (ms16 * 1e-3) / 1e9, 1),
                  "fp16_partial_pct_of_peak": round(
                      100 * alg16 / (ms16p * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
-                 "int4_speedup_vs_fp16": round(ms16 / ms_step, 3)}
+                 "int4_speedup_vs_fp16": round(ms16 / ms_step, 3),
+                 # kernel against kernel: the decode partial on fp16 pages
+                 # against the same launch on INT4 pages (each step adds the
+                 # same few-microsecond merge to both)
+                 "int4_partial_speedup_vs_fp16": round(ms16p / ms_partial, 3)}
         print(f"# fp16 step {ms16 * 1e3:.1f} us (split {split16})", file=sys.stderr, flush=True)
         del fcopies, ws16
 
