@@ -98,3 +98,61 @@ def test_append_and_decode_graph():
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {r}"
         assert torch.equal(kp[0], kc)
+
+
+@pytest.mark.parametrize("hkv,split", [(8, 256), (4, None), (8, None)],
+                         ids=["cooperative_split_k", "per_head", "stream_by_plan"])
+def test_decode_graph_replays_with_new_lengths_tables_and_queries(hkv, split):
+    """A serving loop captures the decode once and, before every replay, writes
+    the step's sequence lengths, block table and queries into the captured
+    buffers (the reference's backend does this for its captured decode steps,
+    F:2185).  Each replay must equal an eager call on the same buffer contents,
+    so nothing of the launch may depend on the lengths seen at capture."""
+    dev = torch.device("cuda")
+    hq, d = 4 * hkv, 128
+    steps = [[1500, 77, 4096], [4200, 1, 2048], [33, 4100, 640], [1, 1, 1], [2049, 3000, 4200]]
+    width = -(-max(max(s) for s in steps) // BS)
+    nb = max(sum(-(-n // BS) for n in s) for s in steps) + 3
+    planes = []
+    for i in range(2):
+        p = kvgen.empty_plane(1, nb, BS, hkv, d, 32)
+        rows = kvgen.randn((nb * BS, hkv, d), 80 + i).float().numpy()
+        kvgen.fill_plane(p, rows, np.arange(nb * BS))
+        planes.append(kvgen.plane_to_torch(p, dev))
+    kp, vp = planes
+    bt = torch.zeros((3, width), dtype=torch.int32, device=dev)
+    sl = torch.zeros(3, dtype=torch.int32, device=dev)
+    q = torch.zeros((3, hq, d), dtype=torch.float16, device=dev)
+
+    def load(r):
+        lens = steps[r]
+        bt.copy_(torch.from_numpy(kvgen.paged_table(lens, BS, nb, 90 + r, max_blocks=width)))
+        sl.copy_(torch.tensor(lens, dtype=torch.int32))
+        q.copy_(kvgen.randn((3, hq, d), 100 + r))
+
+    def step():
+        return K.fused_int4_decode(q, kp[0], vp[0], kp[1], vp[1], bt, sl, hkv, d,
+                                   k_zeros=kp[2], v_zeros=vp[2], asymmetric=True,
+                                   split_tokens=split)
+
+    load(0)
+    step()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):                 # warm the caching allocator off-graph
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got = step()
+    for r in range(len(steps)):
+        load(r)
+        g.replay()
+        torch.cuda.synchronize()
+        replayed = got.clone()
+        want = step()                          # eager on the same buffers
+        torch.cuda.synchronize()
+        assert torch.equal(replayed.view(torch.int16), want.view(torch.int16)), \
+            f"replay {r} lens {steps[r]}"
+        assert torch.isfinite(replayed.float()).all()
