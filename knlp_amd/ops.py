@@ -77,7 +77,38 @@ def _plane(cache: torch.Tensor, scales, zeros, fmt: int, group_size: int) -> KvP
             raise ValueError("asymmetric mode needs fp16 zero-points shaped like the scales")
         p.zeros = zeros.data_ptr()
         p.z_stride_block, p.z_stride_page, p.z_stride_head = zeros.stride()[:3]
+    # shapes for _check_plane (the C ABI carries strides only)
+    p.shape = tuple(cache.shape)
+    p.s_shape = tuple(scales.shape) if fmt != KV_FP16 else None
+    p.z_shape = tuple(zeros.shape) if fmt == KV_INT4_ASYM else None
     return p
+
+
+def _check_plane(p: KvPlane, name: str, num_heads: int, head_size: int) -> None:
+    """Raise ValueError unless the cache of plane ``p`` holds ``num_heads``
+    heads of ``head_size`` elements and its scales / zero-points cover every
+    (block, slot, head, group) of it.  The kernels index these tensors
+    through their strides without bounds checks (as the reference's Triton
+    kernels do), so a cache with fewer heads, a shorter packed axis or
+    smaller scale arrays than the call implies would be read or written out
+    of bounds; this is the host-side guard against that."""
+    shape = getattr(p, "shape", None)
+    if shape is None:
+        return
+    nb, bs, nh, last = shape
+    packed = head_size // 2 if p.format in (KV_INT4_SYM, KV_INT4_ASYM) else head_size
+    if nh < num_heads or last < packed:
+        raise ValueError(f"{name} cache {list(shape)} holds fewer than {num_heads} heads of "
+                         f"{packed} {'bytes' if p.format != KV_FP16 else 'halves'}")
+    if p.format == KV_FP16:
+        return
+    ng = head_size // p.group_size if p.group_size > 0 else 0
+    for what, sh in (("scales", p.s_shape), ("zeros", p.z_shape)):
+        if sh is None:
+            continue
+        if len(sh) != 4 or sh[0] < nb or sh[1] < bs or sh[2] < num_heads or sh[3] < ng:
+            raise ValueError(f"{name} {what} {list(sh)} do not cover a cache of "
+                             f"{list(shape)} with {ng} groups per head")
 
 
 def _src_dtype(t: torch.Tensor) -> int:
@@ -99,12 +130,22 @@ def _slot_dtype(slot_mapping: torch.Tensor) -> int:
 def _append(key, value, kplane, vplane, slot_mapping, clip_ratio, block_size) -> None:
     src = key if key is not None else value
     dt = _src_dtype(src)
-    if key is not None and value is not None and key.dtype != value.dtype:
-        raise ValueError("key and value must share a dtype")
+    if key is not None and value is not None:
+        _src_dtype(value)                      # its own layout checks too
+        if key.dtype != value.dtype:
+            raise ValueError("key and value must share a dtype")
+        if key.shape != value.shape:
+            raise ValueError("key and value must have the same shape")
     slot_mapping = slot_mapping.contiguous()
     num_tokens, num_heads, head_size = src.shape
     if slot_mapping.numel() < num_tokens:
         raise ValueError("slot_mapping shorter than num_tokens")
+    if key is not None:
+        _check_plane(kplane, "key", num_heads, head_size)
+    if value is not None:
+        _check_plane(vplane, "value", num_heads, head_size)
+    if key is not None and value is not None and kplane.shape[1] != vplane.shape[1]:
+        raise ValueError("key and value caches have different block sizes")
     st = lib().knlp_kv_append(
         key.data_ptr() if key is not None else None,
         value.data_ptr() if value is not None else None,
@@ -198,6 +239,10 @@ def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, 
         block_table = block_table.contiguous()
     if seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous():
         seq_lens = seq_lens.to(torch.int32).contiguous()
+    _check_plane(kp, "key", num_kv_heads, head_size)
+    _check_plane(vp, "value", num_kv_heads, head_size)
+    if getattr(kp, "shape", None) and getattr(vp, "shape", None) and kp.shape[1] != vp.shape[1]:
+        raise ValueError("key and value caches have different block sizes")
     L = lib()
     max_context = block_table.shape[1] * block_size
     if split_tokens is None:
@@ -225,9 +270,12 @@ def _decode(query, kp: KvPlane, vp: KvPlane, block_size, block_table, seq_lens, 
     key, value, slot_mapping, clip_ratio = append
     src = key if key is not None else value
     for t in (key, value):
-        if t is not None and (t.dim() != 3 or t.shape[0] < num_seqs or t.stride(2) != 1):
+        if t is not None and (t.dim() != 3 or t.shape[0] < num_seqs or t.stride(2) != 1 or
+                              t.shape[1] != num_kv_heads or t.shape[2] != head_size):
             raise ValueError("key/value must be [num_seqs, num_kv_heads, head_size], "
                              "last axis contiguous")
+    if key is not None and value is not None and key.dtype != value.dtype:
+        raise ValueError("key and value must share a dtype")
     slot_mapping = slot_mapping.contiguous()
     if slot_mapping.numel() < num_seqs:
         raise ValueError("slot_mapping shorter than num_seqs")

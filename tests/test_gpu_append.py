@@ -148,3 +148,102 @@ def test_empty_append_is_noop():
                              asymmetric=True)
     torch.cuda.synchronize()
     assert (g[0].cpu() == 0xA5).all()
+
+
+def _qkv_views(nt, hq, hkv, d, seed, dtype=torch.float16):
+    """key / value as the reference's callers pass them: [T, H, D] views into
+    one fused qkv projection, token stride (hq + 2 hkv) d (F:213-214)."""
+    qkv = kvgen.randn((nt, (hq + 2 * hkv) * d), seed, dtype, 0.0).to(DEV)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(nt, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(nt, hkv, d)
+    assert not k.is_contiguous() and k.stride() == ((hq + 2 * hkv) * d, d, 1)
+    return k, v
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_append_from_qkv_views_bit_exact(dtype):
+    nt, hq, hkv, d, gs, nb, bs = 61, 32, 8, 128, 32, 8, 16
+    k, v = _qkv_views(nt, hq, hkv, d, 41, dtype)
+    slots = _slots(nt, nb, bs, 41)
+    kc, ks, kz = _sentinel_caches(nb, bs, hkv, d, gs, True)
+    vc, vs, vz = _sentinel_caches(nb, bs, hkv, d, gs, True)
+    ref = [t.numpy().copy() for t in (kc, vc, ks, vs, kz, vz)]
+    Q.reshape_and_cache_int4(k.float().cpu().numpy(), v.float().cpu().numpy(), *ref[:4],
+                             slots.numpy(), ref[4], ref[5], asymmetric=True, group_size=gs)
+    g = [t.to(DEV) for t in (kc, vc, ks, vs, kz, vz)]
+    K.reshape_and_cache_int4(k, v, g[0], g[1], g[2], g[3], slots.to(DEV),
+                             g[4], g[5], asymmetric=True, group_size=gs)
+    # INT8 K from the same strided view
+    c8 = torch.full((nb, bs, hkv, d), 0x5A, dtype=torch.int8)
+    s8 = torch.full((nb, bs, hkv, 1), 3.0, dtype=torch.float16)
+    r8, rs8 = c8.numpy().copy(), s8.numpy().copy()
+    Q.reshape_and_cache_k_int8(k.float().cpu().numpy(), r8, rs8, slots.numpy(), group_size=d)
+    g8, gs8 = c8.to(DEV), s8.to(DEV)
+    K.reshape_and_cache_k_int8(k, g8, gs8, slots.to(DEV), group_size=d)
+    torch.cuda.synchronize()
+    for got, want in zip(g, ref):
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint8), want.view(np.uint8))
+    np.testing.assert_array_equal(g8.cpu().numpy(), r8)
+    np.testing.assert_array_equal(gs8.cpu().numpy().view(np.uint16), rs8.view(np.uint16))
+
+
+def test_fused_append_from_qkv_views_matches_separate_append():
+    """append_and_decode with the new token's K/V as strided qkv views writes
+    the same codes as the separate append of contiguous copies."""
+    from knlp_amd import ops
+    hq, hkv, d, gs, bs = 32, 8, 128, 32, 16
+    lens = [300, 45]
+    nb = sum(-(-n // bs) for n in lens) + 2
+    bt = torch.from_numpy(kvgen.paged_table(lens, bs, nb, 77)).to(DEV)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    slots = torch.tensor([int(bt[s, (n - 1) // bs]) * bs + (n - 1) % bs
+                          for s, n in enumerate(lens)], dtype=torch.int64, device=DEV)
+    k, v = _qkv_views(2, hq, hkv, d, 43)
+    q = kvgen.randn((2, hq, d), 44).to(DEV)
+    caches = []
+    for _ in range(2):
+        kc, ks, kz = _sentinel_caches(nb, bs, hkv, d, gs, True)
+        vc, vs, vz = _sentinel_caches(nb, bs, hkv, d, gs, True)
+        caches.append([t.to(DEV) for t in (kc, vc, ks, vs, kz, vz)])
+    a, b = caches
+    out = ops.append_and_decode(q, k, v, slots, a[0], a[1], a[2], a[3], bt, sl,
+                                hkv, d, k_zeros=a[4], v_zeros=a[5], asymmetric=True,
+                                k_group_size=gs, v_group_size=gs)
+    K.reshape_and_cache_int4(k.contiguous(), v.contiguous(), b[0], b[1], b[2],
+                             b[3], slots, b[4], b[5], asymmetric=True, group_size=gs)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+    assert torch.isfinite(out.float()).all()
+
+
+def test_mismatched_shapes_raise_before_launch():
+    """Caches, scales or new-token rows too small for the call raise
+    ValueError on the host (the kernels index them unchecked)."""
+    from knlp_amd import ops
+    hkv, d, gs, nb, bs = 8, 128, 32, 4, 16
+    k, v = _case(5, hkv, d, 3)
+    slots = torch.arange(5, device=DEV)
+    small = [t.to(DEV) for t in _sentinel_caches(nb, bs, 4, d, gs, True)]   # 4 heads
+    full = [t.to(DEV) for t in _sentinel_caches(nb, bs, hkv, d, gs, True)]
+    with pytest.raises(ValueError, match="fewer than"):
+        K.reshape_and_cache_int4(k.to(DEV), v.to(DEV), small[0], full[0], small[1], full[1],
+                                 slots, small[2], full[2], asymmetric=True, group_size=gs)
+    short_scales = full[1][..., :2].contiguous()
+    with pytest.raises(ValueError, match="do not cover"):
+        K.reshape_and_cache_int4(k.to(DEV), v.to(DEV), full[0], full[0].clone(), short_scales,
+                                 full[1].clone(), slots, full[2], full[2].clone(),
+                                 asymmetric=True, group_size=gs)
+    bt = torch.zeros((2, 4), dtype=torch.int32, device=DEV)
+    sl = torch.tensor([10, 20], dtype=torch.int32, device=DEV)
+    q = torch.zeros((2, 32, d), dtype=torch.float16, device=DEV)
+    with pytest.raises(ValueError, match="fewer than"):
+        K.fused_int4_decode(q, small[0], full[0], small[1], full[1], bt, sl, hkv, d,
+                            k_zeros=small[2], v_zeros=full[2], asymmetric=True, group_size=gs)
+    kk = torch.zeros((2, 4, d), dtype=torch.float16, device=DEV)    # 4 of 8 kv heads
+    with pytest.raises(ValueError, match="num_kv_heads"):
+        ops.append_and_decode(q, kk, kk.clone(), slots[:2], full[0], full[0].clone(), full[1],
+                              full[1].clone(), bt, sl, hkv, d, k_zeros=full[2],
+                              v_zeros=full[2].clone(), asymmetric=True, k_group_size=gs,
+                              v_group_size=gs)
+    torch.cuda.synchronize()
