@@ -36,7 +36,12 @@
 //     -8 s (symmetric; -128 s for the biased INT8 codes) folds into a per-row
 //     term sum_t p * z, accumulated in fp32.  Output rows are (g, vg) pairs and
 //     columns are head_dim elements; a column's value is kept only in the row
-//     whose vg is the column's group.
+//     whose vg is the column's group, and hi and lo take one product each.
+//     Group pairs (cooperative kernel, one head set, INT4 V in four groups at
+//     D = 128): a lane reads V as two 16-bit halves per token, so that each
+//     product's 16 columns lie in groups {0, 1} or {2, 3}; the A operand of
+//     a pair has rows (g, group of the pair, hi / lo), and a column sums its
+//     hi and lo rows when the partial is written: half the PV products.
 //     Precision of P': p carries a per-wave power of two 2^k chosen from the
 //     largest V scale seen so far (k lowered, with the accumulators rescaled,
 //     when a larger one arrives), so that max_t P' lies near 2^12..2^14 however
@@ -367,6 +372,11 @@ struct WaveState {
   using ST = SubTile<NCH, NG, KCH, NGK, V16 ? 0 : V8 ? 2 * NCH : NCH>;
   static constexpr bool KZ_USED = KASYM;
   static constexpr bool VZ_USED = VASYM;
+  // Group-pair PV (cooperative kernel, INT4 V in four groups at D = 128):
+  // each product's 16 columns lie in V groups {0, 1} or {2, 3}, and its A
+  // rows are (head, group of the pair, hi / lo), so hi and lo of P' share
+  // one product (8 PV products per tile instead of 16).
+  static constexpr bool PAIRS_OK = !V8 && !V16 && NG == 4 && NCH == 4;
   static_assert(NG % NGK == 0 && (K8 || K16 || NGK == NG),
                 "K scale groups nest in the row groups");
   h8 aq[NCH];          // masked q, A operands of QK (row = col)
@@ -506,7 +516,7 @@ struct WaveState {
   // Probabilities p (times 2^k), P' = p * s_v split into fp16 hi + lo and
   // transposed to the PV A operand (lane = row (g, vg), slots = tokens), and
   // the zero-point term, for the two sub-tiles.
-  template <bool MASK>
+  template <bool MASK, bool PAIRS = false>
   __device__ __forceinline__ void probs(const ST (&st)[2], const bool (&valid)[2],
                                         const float (&score)[2][GPL],
                                         const _Float16 (&svt)[2][NG],
@@ -548,8 +558,11 @@ struct WaveState {
       const float r3 = fmaf(p[3 / NG], sv[3], -static_cast<float>(hi23[1]));
       const h2 lo01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(r0, r1));
       const h2 lo23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(r2, r3));
-      const h4 xhi = {hi01[0], hi01[1], hi23[0], hi23[1]};
-      const h4 xlo = {lo01[0], lo01[1], lo23[0], lo23[1]};
+      // PAIRS: "hi" carries rows (g, vg 0 / 1, hi / lo), "lo" rows (g, vg 2 / 3, hi / lo)
+      const h4 xhi = PAIRS ? h4{hi01[0], lo01[0], hi01[1], lo01[1]}
+                           : h4{hi01[0], hi01[1], hi23[0], hi23[1]};
+      const h4 xlo = PAIRS ? h4{hi23[0], lo23[0], hi23[1], lo23[1]}
+                           : h4{lo01[0], lo01[1], lo23[0], lo23[1]};
       const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
       const f4 thi = __builtin_amdgcn_mfma_f32_16x16x16f16(xhi, eye, zero4, 0, 0, 0);
       const f4 tlo = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo, eye, zero4, 0, 0, 0);
@@ -649,6 +662,7 @@ struct WaveState {
   // pair of columns): the fp16 subnormal bit patterns of slots (2q, 2q + 1),
   // n * 2^-24 for even j and 16 n * 2^-24 for odd j (h == 1), so the
   // accumulators acc[c][1] carry an extra factor 16.
+  template <bool PAIRS = false>
   __device__ __forceinline__ void pv_columns(const uint32_t (&vw)[2][4], const h8& ahi,
                                              const h8& alo) {
     uint32_t u0[4], u1[4];
@@ -671,8 +685,14 @@ struct WaveState {
           bw[q] = ((j % 4) < 2 ? u : u >> 8) & (j % 2 ? kNib16 : kNib1);
         }
         const h8 bv = __builtin_bit_cast(h8, bw);
-        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
-        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
+        if constexpr (PAIRS) {
+          // columns 64 (j / 4) + 4 col + j % 4: groups {0, 1} for j < 4
+          acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 4 ? ahi : alo, bv, acc[c][h],
+                                                             0, 0, 0);
+        } else {
+          acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
+          acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
+        }
       }
     }
   }
@@ -863,7 +883,7 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
 // head g of the set at entry base + g * stride of the workspace.  COLS: the
 // accumulators follow pv_columns' column order, else pv_transposed's.
 template <int D, int NG, bool KASYM, bool VASYM, bool COLS = false, int KCH = D / 32,
-          int NGK = NG, bool V8 = false, bool V16 = false>
+          int NGK = NG, bool V8 = false, bool V16 = false, bool PAIRS = false>
 __device__ __forceinline__ void write_partials_at(
     WaveState<D / 32, NG, KASYM, VASYM, KCH, NGK, V8, V16>& W, const DecodeArgs& a,
     int64_t base, int64_t stride, int col, int blk, int hs = 0) {
@@ -877,8 +897,31 @@ __device__ __forceinline__ void write_partials_at(
   for (int gi = 0; gi < GPL; ++gi) W.lsum[gi] = row_sum16(W.lsum[gi]) * kinv;
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.zacc[e] = row_sum16(W.zacc[e]);
+  // the cooperative kernel's group-pair PV (WaveState::PAIRS_OK, one head set)
+  static_assert(!PAIRS || (COLS && !V8 && !V16 && NG == 4 && D == 128), "pair layout shapes");
+  if constexpr (PAIRS) {
+    const int vgl = col / 8;                 // this lane's group within each pair
+    const int g = blk;
+    if (g < G) {
+      const int64_t row = base + g * stride;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int j = 2 * c + h;
+          const int d = 64 * (j / 4) + 4 * col + j % 4;
+          // constant indices only (a lane-dependent index would move the
+          // accumulators to scratch memory)
+          const f4 v = W.acc[c][h];
+          const float hl = vgl ? v[2] + v[3] : v[0] + v[1];
+          const float z = vgl ? W.zacc[2 * (j / 4) + 1] : W.zacc[2 * (j / 4)];
+          // odd columns carry a factor 16 (pv_columns)
+          a.part_o[row * D + d] = fmaf(hl, h ? 0x1p20f : 0x1p24f, z) * kinv;
+        }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < (PAIRS ? 0 : NCH); ++c) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int d = COLS || V16 ? (D / 16) * col + 2 * c + h
@@ -1249,10 +1292,27 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
 // D/32 bytes at columns (D/16)*col.. of token 16x + 4blk + i.  The four lane
 // blocks read rows 4blk + i, whose chunk swizzles differ, so the 64 lanes
 // hit 64 distinct banks.
-template <class L, int D, class VW>
+template <class L, int D, bool PAIRS = false, class VW>
 __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int col, int blk,
                                             VW (&vw)[2][4]) {
   constexpr int CB = L::HBV / 16;      // V code bytes per lane and token: 8 columns
+  if constexpr (PAIRS) {
+    // columns 4 col .. 4 col + 3 (groups 0-1) in the low half, 64 + 4 col ..
+    // (groups 2-3) in the high half
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int base = L::V_OFF + x * 16 * L::CROWV;
+        const int b0 = wave * L::HBV + 2 * col;
+        const uint32_t lo = *reinterpret_cast<const uint16_t*>(
+            buf + base + L::code_off(L::CROWV, 4 * blk + i, b0));
+        const uint32_t hi = *reinterpret_cast<const uint16_t*>(
+            buf + base + L::code_off(L::CROWV, 4 * blk + i, b0 + D / 4));
+        vw[x][i] = lo | (hi << 16);
+      }
+    return;
+  }
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -1300,16 +1360,22 @@ __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int 
   for (int s = 0; s < NSET; ++s) W[s].template scores<MASK>(st, valid, score[s]);
   if constexpr (PV_PREV) {
 #pragma unroll
-    for (int s = 0; s < NSET; ++s) W[s].pv_columns(vw, ahi[s], alo[s]);
+    for (int s = 0; s < NSET; ++s) {
+      if constexpr (WS::PAIRS_OK && NSET == 1)
+        W[s].template pv_columns<true>(vw, ahi[s], alo[s]);
+      else
+        W[s].pv_columns(vw, ahi[s], alo[s]);
+    }
   }
   // tile i's V replaces tile i - 1's in place once its PV has consumed it
-  coop_read_v<L, D>(cur, wave, col, blk, vw);
+  coop_read_v<L, D, WS::PAIRS_OK && NSET == 1>(cur, wave, col, blk, vw);
   _Float16 sv[2][WS::NGV];
   const float svmax = W[0].template vscales<MASK>(st, valid, sv);
 #pragma unroll
   for (int s = 0; s < NSET; ++s) {
     if (W[s].slow_tile(score[s], svmax)) W[s].slow_step(score[s], svmax);
-    W[s].template probs<MASK>(st, valid, score[s], sv, ahi[s], alo[s]);
+    W[s].template probs<MASK, WS::PAIRS_OK && NSET == 1>(st, valid, score[s], sv, ahi[s],
+                                                          alo[s]);
   }
   // copies issued after tile i + 1's: tiles i + 2 .. min(i + NBUF - 1, ntiles - 1)
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
@@ -1586,8 +1652,12 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
 #undef KNLP_COOP_TILE
 #pragma unroll
   for (int s = 0; s < NSET; ++s) {
-    W[s].pv_columns(vw, ahi[s], alo[s]);
-    write_partials_at<D, NG, KASYM, VASYM, true, KCH, NGK, V8>(
+    constexpr bool PAIRS = std::remove_reference_t<decltype(W[s])>::PAIRS_OK && NSET == 1;
+    if constexpr (PAIRS)
+      W[s].template pv_columns<true>(vw, ahi[s], alo[s]);
+    else
+      W[s].pv_columns(vw, ahi[s], alo[s]);
+    write_partials_at<D, NG, KASYM, VASYM, true, KCH, NGK, V8, false, PAIRS>(
         W[s], a, base0 + s * heads_per_set<NG>() * stride, stride, col, blk,
         s * heads_per_set<NG>());
   }
