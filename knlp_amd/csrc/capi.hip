@@ -1,6 +1,7 @@
 // extern "C" entry points: argument validation, split planning, dispatch.
 // No allocation and no synchronisation happens here; every launch goes to
 // the caller's stream.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 
@@ -232,9 +233,20 @@ int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads, int32_t num_
   if (wide && stream_fits && ragged && num_seqs <= kStreamMaxSeqs &&
       max_context <= kStreamMaxContext)
     return 0;
-  int64_t tok = (total * hgroups + target - 1) / target;
-  if (tok < 64) tok = 64;
-  tok = (tok + 63) / 64 * 64;
+  const auto split_of = [&](int64_t tokens) {
+    int64_t t = (tokens * hgroups + target - 1) / target;
+    if (t < 64) t = 64;
+    return (t + 63) / 64 * 64;
+  };
+  int64_t tok = split_of(total);
+  // A ragged batch left on split-K (planes the stream schedule does not take,
+  // or more sequences than it holds) has splits sized from its real tokens,
+  // but its workspace and grid stay dense: [num_seqs, hq, ceil(max_context /
+  // tok)] partials.  With short sequences in a wide block table that is
+  // gigabytes (256 sequences of 500 tokens in a 131072-token table at 28 q
+  // heads: 1.9 GB).  The split is therefore at least a quarter of the
+  // uniform plan's, which keeps the workspace within about 4x of it.
+  tok = std::max(tok, (split_of(rect) / 4 + 63) / 64 * 64);
   if (tok > max_context) tok = (static_cast<int64_t>(max_context) + 63) / 64 * 64;
   return static_cast<int32_t>(tok);
 }
@@ -268,7 +280,7 @@ int knlp_kv_decode_kernel_kind(int32_t num_q_heads, int32_t num_kv_heads, int32_
                                int32_t v_group_size, int32_t q_dtype) {
   if (num_kv_heads <= 0 || num_q_heads % num_kv_heads) return KNLP_ERR_SHAPE;
   const int g = num_q_heads / num_kv_heads;
-  if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
+  if (check_head_size(head_size)) return KNLP_ERR_SHAPE;
   bool mfma = mfma_supported(g, head_size, k_format, k_group_size, v_format, v_group_size,
                              q_dtype == KNLP_DT_BF16);
   // INT8 K, INT8 V (with INT4 / INT8 K) and two head sets exist only on the
@@ -371,8 +383,11 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
   }
   if (app != nullptr) a.app = *app;
   hipStream_t hs = static_cast<hipStream_t>(stream_ptr);
-  const bool mfma = kind == 1 && softmax_scale > 0.0f && mfma_layout_ok(kp, head_size, block_size) &&
+  // (any finite softmax scale: the matrix-core kernels fold a negative one's
+  // sign into q and treat 0 as uniform weights)
+  const bool mfma = kind == 1 && mfma_layout_ok(kp, head_size, block_size) &&
                     mfma_layout_ok(vp, head_size, block_size);
+  int32_t* fallback_hdr = nullptr;
   if (stream && !(mfma && stream_supported(a, head_size))) {
     // Planes only the split schedule takes (fp16 K, Hkv % 8 != 0, a sparse
     // layout): split-K inside the stream workspace, [num_seqs, hq, ns] over
@@ -387,11 +402,15 @@ int decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_seq,
     a.split_tokens = static_cast<int>(split);
     a.num_splits = static_cast<int>((max_context + split - 1) / split);
     if (a.num_splits > kMaxGridYZ) return KNLP_ERR_SHAPE;
-    const StreamViews v = stream_views(workspace, num_seqs, num_q_heads, head_size, P);
-    if ((st = launch_stream_header(v.hdr, 0, a.split_tokens, a.num_splits, hs))) return st;
+    fallback_hdr = stream_views(workspace, num_seqs, num_q_heads, head_size, P).hdr;
   }
-  if (mfma) return launch_decode_mfma(a, head_size, hs);
-  return launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), hs);
+  // The decode launch first: a shape it cannot serve returns before anything
+  // is launched.  The fallback's header (read only by the merge, later on the
+  // same stream) follows it.
+  st = mfma ? launch_decode_mfma(a, head_size, hs)
+            : launch_decode_valu(a, head_size, heads_per_block(num_kv_heads), hs);
+  if (st || fallback_hdr == nullptr) return st;
+  return launch_stream_header(fallback_hdr, 0, a.split_tokens, a.num_splits, hs);
 }
 
 }  // namespace
@@ -412,14 +431,21 @@ int knlp_kv_decode_partial(const void* query, int32_t q_dtype, int64_t q_stride_
                         split_tokens, workspace, workspace_bytes, nullptr, stream);
 }
 
-int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const int32_t* seq_lens,
-                         int32_t num_seqs, int32_t num_q_heads, int32_t head_size,
-                         int32_t max_context, int32_t split_tokens, void* out, int32_t out_dtype,
-                         int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The merge launch, or with dry = true only its argument checks (the fused
+// entry points run those before the partial launch, so that no negative
+// status follows a launch).
+int decode_merge(const void* workspace, int64_t workspace_bytes, const int32_t* seq_lens,
+                 int32_t num_seqs, int32_t num_q_heads, int32_t head_size, int32_t max_context,
+                 int32_t split_tokens, void* out, int32_t out_dtype, int64_t o_stride_seq,
+                 int64_t o_stride_head, void* stream, bool dry) {
   if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
   if (num_seqs < 0 || num_q_heads <= 0 || max_context <= 0 || split_tokens < 0)
     return KNLP_ERR_SHAPE;
-  if (head_size != 64 && head_size != 128 && head_size != 256) return KNLP_ERR_SHAPE;
+  if (check_head_size(head_size)) return KNLP_ERR_SHAPE;
   if (num_seqs == 0) return KNLP_OK;
   if (num_seqs > kMaxGridYZ) return KNLP_ERR_SHAPE;
   if (out == nullptr || seq_lens == nullptr) return KNLP_ERR_ARG;
@@ -430,6 +456,7 @@ int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const i
     if (workspace == nullptr ||
         workspace_bytes < stream_workspace_bytes(num_seqs, num_q_heads, head_size, P))
       return KNLP_ERR_WORKSPACE;
+    if (dry) return KNLP_OK;
     const StreamViews v =
         stream_views(const_cast<void*>(workspace), num_seqs, num_q_heads, head_size, P);
     // a row holds about P / rows + 1 entries, rows >= num_seqs
@@ -441,12 +468,26 @@ int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const i
   const int ns = (max_context + split_tokens - 1) / split_tokens;
   const int64_t need = workspace_floats(num_seqs, num_q_heads, head_size, ns) * 4;
   if (workspace == nullptr || workspace_bytes < need) return KNLP_ERR_WORKSPACE;
+  if (dry) return KNLP_OK;
   float *po, *pml;
   workspace_views(const_cast<void*>(workspace), num_seqs, num_q_heads, head_size, ns, &po, &pml);
   return launch_merge(po, pml, seq_lens, num_seqs, num_q_heads, head_size, max_context,
                       split_tokens, ns, out,
                       out_dtype == KNLP_DT_BF16, o_stride_seq, o_stride_head,
                       static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int knlp_kv_decode_merge(const void* workspace, int64_t workspace_bytes, const int32_t* seq_lens,
+                         int32_t num_seqs, int32_t num_q_heads, int32_t head_size,
+                         int32_t max_context, int32_t split_tokens, void* out, int32_t out_dtype,
+                         int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
+  return decode_merge(workspace, workspace_bytes, seq_lens, num_seqs, num_q_heads, head_size,
+                      max_context, split_tokens, out, out_dtype, o_stride_seq, o_stride_head,
+                      stream, false);
 }
 
 int knlp_kv_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
@@ -457,9 +498,11 @@ int knlp_kv_decode(const void* query, int32_t q_dtype, int64_t q_stride_seq,
                    int32_t max_context, float softmax_scale, int32_t split_tokens,
                    void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
                    int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
-  if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
-  if (num_seqs > 0 && out == nullptr) return KNLP_ERR_ARG;
-  int st = knlp_kv_decode_partial(query, q_dtype, q_stride_seq, q_stride_head, num_seqs,
+  int st = decode_merge(workspace, workspace_bytes, seq_lens, num_seqs, num_q_heads, head_size,
+                        max_context, split_tokens, out, out_dtype, o_stride_seq, o_stride_head,
+                        stream, true);
+  if (st) return st;
+  st = knlp_kv_decode_partial(query, q_dtype, q_stride_seq, q_stride_head, num_seqs,
                                   num_q_heads, num_kv_heads, head_size, key_cache, value_cache,
                                   block_table, bt_stride_seq, seq_lens, block_size, max_context,
                                   softmax_scale, split_tokens, workspace, workspace_bytes,
@@ -483,15 +526,16 @@ int knlp_kv_append_decode(const void* query, int32_t q_dtype, int64_t q_stride_s
                           float softmax_scale, int32_t split_tokens, void* workspace,
                           int64_t workspace_bytes, void* out, int32_t out_dtype,
                           int64_t o_stride_seq, int64_t o_stride_head, void* stream) {
-  if (out_dtype != KNLP_DT_F16 && out_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
-  if (num_seqs > 0 && out == nullptr) return KNLP_ERR_ARG;
+  int st = decode_merge(workspace, workspace_bytes, seq_lens, num_seqs, num_q_heads, head_size,
+                        max_context, split_tokens, out, out_dtype, o_stride_seq, o_stride_head,
+                        stream, true);
+  if (st) return st;
   if (num_seqs == 0) return KNLP_OK;
   if (src_dtype != KNLP_DT_F16 && src_dtype != KNLP_DT_BF16) return KNLP_ERR_DTYPE;
   if (slot_dtype != KNLP_DT_I32 && slot_dtype != KNLP_DT_I64) return KNLP_ERR_DTYPE;
   if (key == nullptr && value == nullptr) return KNLP_ERR_ARG;
   if (slot_mapping == nullptr) return KNLP_ERR_ARG;
   if (!(clip_ratio >= 0.0f) || std::isinf(clip_ratio)) return KNLP_ERR_ARG;
-  int st;
   if (key != nullptr) {
     if ((st = check_plane(key_cache, head_size, false))) return st;
     if (key_cache->format == KNLP_KV_FP16 && src_dtype != KNLP_DT_F16) return KNLP_ERR_DTYPE;
@@ -555,15 +599,24 @@ __device__ __align__(256) uint8_t scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch[kMaxDevices];
 
-// This device's copy of `scratch`, looked up once per device (with that
-// device current, as hipGetDevice reports it); nullptr on failure.
-void* device_scratch() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+// The copy of `scratch` on the device that `stream` belongs to (the null
+// stream: the current device), looked up once per device with that device
+// current; nullptr on failure.
+void* device_scratch(hipStream_t stream) {
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  hipDevice_t dev = cur;
+  if (stream != nullptr && hipStreamGetDevice(stream, &dev) != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
   void* p = g_scratch[dev].load(std::memory_order_acquire);
   if (p != nullptr) return p;
+  // hipGetSymbolAddress answers for the current device: make the stream's
+  // device current for the lookup and restore the caller's afterwards
+  if (dev != cur && hipSetDevice(dev) != hipSuccess) return nullptr;
   void* q = nullptr;
-  if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || q == nullptr) return nullptr;
+  const bool ok = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) == hipSuccess && q != nullptr;
+  if (dev != cur && hipSetDevice(cur) != hipSuccess) return nullptr;
+  if (!ok) return nullptr;
   g_scratch[dev].store(q, std::memory_order_release);   // a racing store writes the same value
   return q;
 }
@@ -591,7 +644,7 @@ extern "C" int knlp_kv_decode_noalloc(const void* query, int32_t q_dtype, int64_
                                                       max_context, split_tokens);
   if (need < 0) return static_cast<int>(need);
   if (need > kScratchBytes) return KNLP_ERR_WORKSPACE;
-  void* ws = device_scratch();
+  void* ws = device_scratch(static_cast<hipStream_t>(stream));
   if (ws == nullptr) return KNLP_ERR_LAUNCH;
   return knlp_kv_decode(query, q_dtype, q_stride_seq, q_stride_head, num_seqs, num_q_heads,
                         num_kv_heads, head_size, key_cache, value_cache, block_table,

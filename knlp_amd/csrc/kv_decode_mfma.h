@@ -799,11 +799,17 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   // qscale = 2^(14 - e) with max|q_head| < 2^e: exact for every element down
   // to 2^-28 of the head's maximum (fp16 holds bf16's 8-bit mantissa), and
   // the scale leaves the scores through the row's softmax scale.
+  // The online softmax below tracks each row's maximum score, which needs a
+  // positive scale: a negative softmax scale enters as -q with |scale|
+  // (negation is exact), and a zero scale as q = 0 (every score 0, so the
+  // weights are uniform over the valid tokens) with any positive scale.
+  const bool qneg = a.scale_log2 < 0.0f;
+  const bool qzero = a.scale_log2 == 0.0f;
   float qpart = 0.0f;
   float qscale = 1.0f;
   {
     const int r = col;
-    const bool on = r < rows && ((D / 4) * blk) / gs == r % NG;
+    const bool on = r < rows && ((D / 4) * blk) / gs == r % NG && !qzero;
     uint16_t qv[D / 4];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
@@ -830,10 +836,10 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int el = 8 * c + (K16 ? e : K8 ? kByteK8[e] : kNibK[e]);
-        const _Float16 v =
-            !on ? _Float16(0)
-                : a.q_bf16 ? static_cast<_Float16>(bf16_bits_to_float(qv[el]) * qscale)
-                           : __builtin_bit_cast(_Float16, qv[el]);
+        _Float16 v = !on ? _Float16(0)
+                     : a.q_bf16 ? static_cast<_Float16>(bf16_bits_to_float(qv[el]) * qscale)
+                                : __builtin_bit_cast(_Float16, qv[el]);
+        if (qneg) v = -v;
         // odd nibbles arrive as 16 n: their q slot holds q / 16 (exact
         // unless |q| < 2^-10, where the fp16 subnormal keeps an absolute
         // error below 2^-25); INT8 codes arrive as n + 128
@@ -874,7 +880,7 @@ __device__ __forceinline__ void init_wave(WaveState<D / 32, NG, KASYM, VASYM, KC
   for (int gi = 0; gi < GPL; ++gi) {
     const float qs = __shfl(qscale, 4 * blk + gi * NG, kWave);
     // INT4 / INT8 codes enter as n * 2^-24; fp16 K as itself
-    W.sl2[gi] = a.scale_log2 * (K16 ? 1.0f : 0x1p24f) / qs;
+    W.sl2[gi] = (qzero ? 1.0f : fabsf(a.scale_log2)) * (K16 ? 1.0f : 0x1p24f) / qs;
     W.thr[gi] = kRescaleLog2 / W.sl2[gi];
   }
 }

@@ -317,6 +317,7 @@ int launch_decode_valu(const DecodeArgs& a, int head_size, int heads_per_block,
   const dim3 block(kWave * heads_per_block);
   int st;
   switch (head_size) {
+    case 32: st = launch_gb<32>(a, grid, block, stream); break;
     case 64: st = launch_gb<64>(a, grid, block, stream); break;
     case 128: st = launch_gb<128>(a, grid, block, stream); break;
     case 256: st = launch_gb<256>(a, grid, block, stream); break;

@@ -245,6 +245,7 @@ int launch_merge(const float* part_o, const float* part_ml, const int32_t* seq_l
   case D:                                                                                 \
     if (hpw == 8) { KNLP_MERGE_W(D, 8) } else { KNLP_MERGE_W(D, 4) }                      \
     break;
+      KNLP_MERGE_WD(32)
       KNLP_MERGE_WD(64)
       KNLP_MERGE_WD(128)
       KNLP_MERGE_WD(256)
@@ -271,6 +272,7 @@ int launch_merge(const float* part_o, const float* part_ml, const int32_t* seq_l
     else if (nw == 8) { KNLP_MERGE_NW(D, 8) }                                           \
     else { KNLP_MERGE_NW(D, 16) }                                                       \
     break;
+    KNLP_MERGE_D(32)
     KNLP_MERGE_D(64)
     KNLP_MERGE_D(128)
     KNLP_MERGE_D(256)

@@ -117,7 +117,10 @@ class FusedInt4AttentionBackend(AttentionBackend):
 
     @classmethod
     def supports_head_size(cls, head_size: int) -> bool:
-        return head_size > 0 and head_size % config.GROUP_SIZE == 0
+        # F:2168-2171 asks D % GROUP_SIZE == 0; its kernels also need a power
+        # of two (tl.arange(0, HALF_HD), F:729-735).  These are the head sizes
+        # this library's append and decode both take.
+        return head_size in (32, 64, 128, 256) and head_size % config.GROUP_SIZE == 0
 
     @classmethod
     def supports_attn_type(cls, attn_type: str) -> bool:

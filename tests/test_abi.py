@@ -12,6 +12,21 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "knlp_int4kv.h")
 
 
+def _gpu_visible() -> bool:
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+# Tests whose calls pass validation with made-up device addresses: without a
+# GPU the launch itself fails (KNLP_ERR_LAUNCH); with one it would run a
+# kernel on those addresses, so they run only where no GPU is visible.
+no_gpu_only = pytest.mark.skipif(_gpu_visible(), reason="passes made-up device addresses "
+                                                        "that a visible GPU would launch on")
+
+
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
@@ -115,6 +130,7 @@ def test_ops_require_device_tensors():
                               torch.ones(1, dtype=torch.int32), 1, 64)
 
 
+@no_gpu_only
 def test_fp16_plane_group_size_is_not_read():
     """An fp16 plane has no scales; a group_size of 0 in it must not reach a
     division (it used to end the process with SIGFPE on the dispatch path).
@@ -244,3 +260,132 @@ def test_argument_validation_fuzz_never_crashes():
                               pick([0, 64]), pick([0, 0x60000]), bs, mc, pick([0.088, -1.0]),
                               split, None, 0, pick([0, 0x70000]), pick([0, 1]), 4096, 128, None)
         assert st in statuses and (st != 0 or S == 0), (st, S, hq, hkv, d, kf, vf, kgs, vgs)
+
+
+def _ws_of_plan(L, S, hkv, hq, d, mc, total, kf, kg, vf, vg):
+    sp = L.knlp_kv_decode_plan(S, hkv, hq, d, mc, total, kf, kg, vf, vg)
+    assert sp >= 0
+    return sp, L.knlp_kv_decode_workspace_bytes(S, hq, d, mc, sp)
+
+
+def test_ragged_split_plan_keeps_workspace_bounded():
+    """A ragged batch that stays on split-K (no stream schedule: Hkv % 8 != 0,
+    fp16 K, or more than 1024 sequences) gets splits sized from its real
+    tokens, but its workspace is dense over max_context: the plan keeps it
+    within about 4x of the uniform plan's (before: 1.9 GB for 256 sequences
+    of 500 tokens in a 131072-token table)."""
+    L = _lib.lib()
+    a4, f16, i8 = _lib.KV_INT4_ASYM, _lib.KV_FP16, _lib.KV_INT8_SYM
+    cases = [
+        (256, 4, 28, 128, 131072, 256 * 500, a4, 32, a4, 32),       # Hkv % 8 != 0
+        (256, 4, 28, 128, 131072, 256 * 100, f16, 128, a4, 32),     # fp16 K
+        (1100, 8, 32, 128, 131072, 1100 * 500, a4, 32, a4, 32),     # > 1024 sequences
+        (1100, 4, 28, 128, 65536, 1100 * 100, f16, 128, i8, 128),
+        (2000, 8, 40, 128, 32768, 2000 * 64, i8, 128, a4, 32),
+    ]
+    for S, hkv, hq, d, mc, total, kf, kg, vf, vg in cases:
+        sp, ws = _ws_of_plan(L, S, hkv, hq, d, mc, total, kf, kg, vf, vg)
+        sp_u, ws_u = _ws_of_plan(L, S, hkv, hq, d, mc, S * mc, kf, kg, vf, vg)
+        assert sp > 0 and sp_u > 0 and sp % 64 == 0
+        # ceil(mc / sp) <= 4 ceil(mc / sp_u) + 4 splits
+        assert ws <= 4 * ws_u + 4 * S * hq * (d + 2) * 4, (S, hkv, sp, sp_u, ws, ws_u)
+        assert ws < 256 << 20, (S, hkv, ws)
+    # uniform batches and ragged batches on the stream schedule are unchanged
+    assert L.knlp_kv_decode_plan(8, 8, 32, 128, 32768, 8 * 32768, a4, 32, a4, 32) == 1024
+    assert L.knlp_kv_decode_plan(64, 8, 32, 128, 16384, 64 * 8192, a4, 32, a4, 32) == 0
+    # ... and a long sequence among short ones still gets short splits
+    # relative to the table (not the uniform plan's)
+    sp, _ = _ws_of_plan(L, 128, 4, 28, 128, 100000 // 64 * 64, 100000 + 127 * 500, a4, 32, a4,
+                        32)
+    sp_u, _ = _ws_of_plan(L, 128, 4, 28, 128, 100000 // 64 * 64, 128 * (100000 // 64 * 64),
+                          a4, 32, a4, 32)
+    assert sp < sp_u
+
+
+@no_gpu_only
+def test_stream_fallback_shape_error_comes_before_any_launch():
+    """The stream schedule (split 0) on planes only split-K takes falls back to
+    split-K inside the stream workspace.  When that fallback cannot serve the
+    shape either (the VALU kernel takes at most 8 query heads per kv head,
+    here 16 on a layout the matrix-core kernels do not take), the status is
+    a shape error and nothing is launched: the fallback's header kernel,
+    which once ran first, now follows the decode launch."""
+    L = _lib.lib()
+    kp, vp = _plane(gs=128, data=0x1004), _plane(gs=128)
+    for p in (kp, vp):
+        p.stride_block, p.stride_page, p.stride_head = 16 * 2 * 64, 2 * 64, 64
+        p.s_stride_block, p.s_stride_page, p.s_stride_head = 16 * 2, 2, 1
+        p.z_stride_block, p.z_stride_page, p.z_stride_head = 16 * 2, 2, 1
+    assert L.knlp_kv_decode_kernel_kind(32, 2, 128, _lib.KV_INT4_ASYM, 128, _lib.KV_INT4_ASYM,
+                                        128, 0) == 1
+    for fn in ("knlp_kv_decode", "knlp_kv_decode_partial"):
+        args = [0x10000, _lib.DT_F16, 32 * 128, 128, 2, 32, 2, 128, ctypes.byref(kp),
+                ctypes.byref(vp), 0x50000, 2048, 0x60000, 16, 32768, 0.088, 0, 0x100000,
+                1 << 40]
+        if fn == "knlp_kv_decode":
+            args += [0x70000, _lib.DT_F16, 32 * 128, 128]
+        st = getattr(L, fn)(*args, None)
+        assert st == _lib.ERR_SHAPE, (fn, st)
+
+
+def test_fused_entry_points_check_the_merge_before_the_partial():
+    """knlp_kv_decode and knlp_kv_append_decode validate the merge's own
+    arguments (output pointer, dtype, alignment) before the partial launch,
+    so a merge error is never returned after a launch."""
+    L = _lib.lib()
+    kp, vp = _plane(), _plane()
+
+    def dec(out=0x70000, odt=_lib.DT_F16):
+        return L.knlp_kv_decode(0x10000, _lib.DT_F16, 32 * 128, 128, 8, 32, 8, 128,
+                                ctypes.byref(kp), ctypes.byref(vp), 0x50000, 2048, 0x60000,
+                                16, 32768, 0.088, 1024, 0x100000, 1 << 40, out, odt,
+                                32 * 128, 128, None)
+
+    def app(out=0x70000, odt=_lib.DT_F16):
+        return L.knlp_kv_append_decode(
+            0x10000, _lib.DT_F16, 32 * 128, 128, 8, 32, 8, 128, 0x80000, 0x90000,
+            _lib.DT_F16, 1024, 128, 1024, 128, 0xA0000, _lib.DT_I64, 0.0, ctypes.byref(kp),
+            ctypes.byref(vp), 0x50000, 2048, 0x60000, 16, 32768, 0.088, 1024, 0x100000,
+            1 << 40, out, odt, 32 * 128, 128, None)
+
+    for f in (dec, app):
+        assert f(out=0x70001) == _lib.ERR_ALIGN
+        assert f(out=None) == _lib.ERR_ARG
+        assert f(odt=_lib.DT_I32) == _lib.ERR_DTYPE
+
+
+@no_gpu_only
+def test_softmax_scale_of_any_sign_keeps_matrix_core_shapes():
+    """Shapes that only the matrix-core kernels serve (two head sets of 16
+    query heads per kv head: the VALU kernel takes at most 8) pass
+    validation with a negative or zero softmax scale too: the kernels fold a
+    negative scale's sign into q and treat 0 as uniform weights.  (Without a
+    GPU the call gets as far as the launch.)"""
+    L = _lib.lib()
+    kp, vp = _plane(gs=64), _plane(gs=64)
+    for p in (kp, vp):
+        p.s_stride_block, p.s_stride_page, p.s_stride_head = 16 * 8 * 2, 8 * 2, 2
+        p.z_stride_block, p.z_stride_page, p.z_stride_head = 16 * 8 * 2, 8 * 2, 2
+    assert L.knlp_kv_decode_kernel_kind(128, 8, 128, _lib.KV_INT4_ASYM, 64, _lib.KV_INT4_ASYM,
+                                        64, 0) == 1
+    for scale in (0.088, -0.088, 0.0):
+        st = L.knlp_kv_decode(0x10000, _lib.DT_F16, 128 * 128, 128, 8, 128, 8, 128,
+                              ctypes.byref(kp), ctypes.byref(vp), 0x50000, 2048, 0x60000, 16,
+                              32768, scale, 1024, 0x100000, 1 << 40, 0x70000, _lib.DT_F16,
+                              128 * 128, 128, None)
+        assert st in (_lib.OK, _lib.ERR_LAUNCH), (scale, st)
+    for bad in (float("inf"), float("nan")):
+        st = L.knlp_kv_decode(0x10000, _lib.DT_F16, 128 * 128, 128, 8, 128, 8, 128,
+                              ctypes.byref(kp), ctypes.byref(vp), 0x50000, 2048, 0x60000, 16,
+                              32768, bad, 1024, 0x100000, 1 << 40, 0x70000, _lib.DT_F16,
+                              128 * 128, 128, None)
+        assert st == _lib.ERR_ARG
+
+
+def test_head_size_32_decodes():
+    """D = 32 (which the append takes) decodes too, on the VALU kernel."""
+    L = _lib.lib()
+    a4 = _lib.KV_INT4_ASYM
+    assert L.knlp_kv_decode_kernel_kind(8, 8, 32, a4, 32, a4, 32, 0) == 0
+    assert L.knlp_kv_decode_kernel_kind(8, 8, 32, a4, 16, a4, 16, 0) == 0
+    assert L.knlp_kv_decode_kernel_kind(8, 8, 96, a4, 32, a4, 32, 0) == _lib.ERR_SHAPE

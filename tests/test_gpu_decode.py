@@ -3,9 +3,10 @@ dequantise-then-SDPA path (scripts/v35_h100_bench.py:376-387; F:656-979,
 F:1318-1554 and the precision variants).
 
 Tolerance (tests/tolerance.py): max |gpu - oracle| <= 2e-3 against the
-oracle's fp32 result before output rounding, plus half an fp16 ulp of output
-rounding (2^-10 |oracle|) only where |oracle| > 2; bf16 outputs carry half a
-bf16 ulp (2^-8 |oracle|).  Every check records its achieved max-abs error.
+oracle's fp32 result before output rounding, plus half an fp16 ulp of the
+GPU's output rounding (2^-11 |oracle|) only where |oracle| > 2; bf16 outputs
+carry their two roundings (fp32 -> fp16 -> bf16: (2^-8 + 2^-11) |oracle|).
+Every check records its achieved max-abs error.
 """
 import os
 import zlib
@@ -144,6 +145,10 @@ CASES = [
     ("fp16_fp16_d64", [700, 16], 16, 8, 64, 3, 3, 64, 64),
     ("fp16_fp16_mha", [333], 6, 6, 128, 3, 3, 128, 128),
     ("fp16_fp16_d256_valu", [400], 32, 8, 256, 3, 3, 256, 256),
+    # head size 32 (VALU kernel): one group of 32 or two of 16
+    ("d32_g32_asym", [700, 33, 1], 8, 2, 32, 1, 1, 32, 32),
+    ("d32_g16_sym_mha", [400], 4, 4, 32, 0, 0, 16, 16),
+    ("d32_kint8_vint4", [300, 65], 16, 8, 32, 2, 1, 32, 16),
 ]
 
 
@@ -402,3 +407,49 @@ def test_decode_fp16_sdpa_matches_reference_sdpa(max_ctx):
         ref.append((p @ vv)[:, 0, :])
     ref = torch.stack(ref).numpy()
     tolerance.check(f"decode_fp16_sdpa_{max_ctx}", out.float().cpu().numpy(), ref)
+
+
+SCALE_CASES = [
+    # name, seq_lens, hq, hkv, d, kfmt, vfmt, kgs, vgs, split (None: the plan)
+    ("coop_split", [1500, 300], 32, 8, 128, 1, 1, 32, 32, 256),
+    ("coop_stream", [1500, 300, 77], 32, 8, 128, 1, 1, 32, 32, 0),
+    ("coop_two_sets", [700, 33], 40, 8, 128, 1, 1, 32, 32, None),
+    ("coop_g16_g64_two_sets", [600], 128, 8, 128, 1, 1, 64, 64, None),
+    ("coop_kint8", [900, 5], 40, 8, 128, 2, 1, 128, 32, None),
+    ("perhead_hkv4", [900, 17], 16, 4, 128, 1, 1, 32, 32, None),
+    ("perhead_kfp16", [500], 32, 8, 128, 3, 1, 128, 32, None),
+]
+
+
+@pytest.mark.parametrize("scale", [-0.125, 0.0], ids=["negative", "zero"])
+@pytest.mark.parametrize("case", SCALE_CASES, ids=[c[0] for c in SCALE_CASES])
+def test_softmax_scale_any_sign_on_matrix_cores(case, scale):
+    """A negative softmax scale enters the matrix-core kernels as -q with
+    |scale|; a zero scale as q = 0, every token weighted alike.  Negative:
+    against the oracle at that scale.  Zero: against the closed form, the
+    mean of the dequantised V rows of each sequence."""
+    from knlp_amd import ops
+    name, seq_lens, hq, hkv, d, kf, vf, kgs, vgs, split = case
+    assert K.decode_kernel_kind(hq, hkv, d, kf, kgs, vf, vgs) == "mfma"
+    seed = zlib.crc32(name.encode()) % 1000
+    bt, kp, vp = _build(seq_lens, hq, hkv, d, kf, vf, kgs, vgs, seed)
+    q = _query(len(seq_lens), hq, d, seed)
+    fmt = {"int4_sym": 0, "int4_asym": 1, "int8": 2, "fp16": 3}
+    kd, ks, kz = kvgen.plane_to_torch(kp, DEV)
+    vd, vs, vz = kvgen.plane_to_torch(vp, DEV)
+    print(f"scale case {name} scale={scale} split={split}", flush=True)
+    out = ops._decode(q.to(DEV), ops._plane(kd, ks, kz, fmt[kp["format"]], kp["group_size"]),
+                      ops._plane(vd, vs, vz, fmt[vp["format"]], vp["group_size"]), kd.shape[1],
+                      torch.from_numpy(bt).to(DEV),
+                      torch.tensor(seq_lens, dtype=torch.int32, device=DEV), hkv, d,
+                      scale=scale, split_tokens=split)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    if scale != 0.0:
+        ref = A.decode_reference(q.float().numpy(), kp, vp, bt, seq_lens, scale=scale,
+                                 round_output=False)
+    else:
+        deq = A.dequant_plane(vp)
+        ref = np.stack([np.repeat(A.gather_sequence(deq, bt[s], n).astype(np.float64).mean(0),
+                                  hq // hkv, axis=0) for s, n in enumerate(seq_lens)])
+    tolerance.check(f"scale_{name}_{scale:g}", got, ref)

@@ -15,6 +15,8 @@ import sys
 import pytest
 import torch
 
+from knlp_amd import _lib
+
 from knlp_amd import config, kv_layout
 
 STUB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "vllm_stub")
@@ -100,6 +102,14 @@ def test_backend_surface(vb, monkeypatch):
     assert not B.supports_kv_cache_dtype("fp8")
     assert B.supports_head_size(128) and B.supports_head_size(64)
     assert not B.supports_head_size(100) and not B.supports_head_size(0)
+    # every admitted head size is one the decode takes (D = 32 included), and
+    # none it rejects (96 = 3 * 32 passes F's divisibility test alone)
+    L = _lib.lib()
+    for d in range(16, 513, 16):
+        if B.supports_head_size(d):
+            assert L.knlp_kv_decode_kernel_kind(8, 8, d, 1, 32, 1, 32, 0) in (0, 1), d
+    assert B.supports_head_size(32) and not B.supports_head_size(96)
+    assert not B.supports_head_size(512)
     assert B.supports_attn_type("decoder") and not B.supports_attn_type("encoder")
     assert B.get_kv_cache_shape(5, 16, 8, 128) == (2, 5, 16, 8, 128)
     monkeypatch.setattr(config, "REPLACE_CACHE", True)

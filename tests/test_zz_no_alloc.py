@@ -81,6 +81,19 @@ def test_noalloc_stream_schedule_twice():
         assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
 
 
+def test_noalloc_on_a_side_stream():
+    """The scratch is the copy on the stream's device, looked up through the
+    stream (a non-null one here), and the call runs on that stream."""
+    q, planes, bt, sl = _case([1800, 500, 64], 32, 8, 128, 1, 32, 99)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    for split in (256, 0):
+        print(f"noalloc side-stream call: split={split}", flush=True)
+        with torch.cuda.stream(side):
+            ref, out = _both(q, planes, bt, sl, 8, 128, 1, 32, split)
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+
 def test_noalloc_rejects_shapes_beyond_the_scratch():
     L = _lib.lib()
     q, planes, bt, sl = _case([64], 32, 8, 128, 1, 32, 95)
