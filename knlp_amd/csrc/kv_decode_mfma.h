@@ -1407,6 +1407,37 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   return static_cast<uint32_t>(v);
 }
 
+// floor(x T / Pe) for 0 <= x <= Pe <= 2^16: with T = q Pe + r, that is
+// x q + floor(x r / Pe), x r < 2^32.  Two 32-bit divisions when T fits 32
+// bits (a 64-bit division is a long dependent sequence, and the stream
+// schedule's start runs several before its first copy).
+__device__ __forceinline__ uint64_t share_bound(uint32_t x, uint64_t T, uint32_t Pe) {
+  uint64_t q;
+  uint32_t r;
+  if ((T >> 32) == 0) {
+    const uint32_t t = static_cast<uint32_t>(T);
+    q = t / Pe;
+    r = t - static_cast<uint32_t>(q) * Pe;
+  } else {
+    q = T / Pe;
+    r = static_cast<uint32_t>(T - q * Pe);
+  }
+  return x * q + (x * r) / Pe;
+}
+
+// The block holding flattened position t < T of the stream schedule: the b
+// with floor(b T / Pe) <= t < floor((b + 1) T / Pe), i.e.
+// floor((t Pe + Pe - 1) / T).  For T < 2^32 and Pe <= 2^16 the numerator
+// (< 2^48) and T are exact in fp64 and the quotient is below 2^16, so the
+// correctly rounded fp64 quotient cannot cross an integer: the floor is
+// exact.
+__device__ __forceinline__ int block_of_position(uint64_t t, uint64_t T, uint32_t Pe) {
+  const uint64_t num = t * Pe + Pe - 1;
+  if ((T >> 32) == 0)
+    return static_cast<int>(__builtin_floor(static_cast<double>(num) / static_cast<double>(T)));
+  return static_cast<int>(num / T);
+}
+
 // Where a stream-schedule block starts: the sequence s holding flattened
 // position f (rows of sequence s are cost + n_s positions long, nhg rows per
 // sequence, laid end to end in sequence order), its first position sbase,
@@ -1429,30 +1460,54 @@ struct StreamStart {
       const int i = kWave * k + lane;
       len_k[k] = (k < nk && i < a.num_seqs) ? a.seq_lens[i] : 0;
     }
-    // all rows' tiles (nhg rows per sequence)
+    // all rows' tiles (nhg rows per sequence), and whether every non-empty
+    // sequence has the same tile count (that of lane 0's first non-empty one)
+    uint32_t incl[KMAX];
     uint64_t tiles = 0;
+    uint32_t nonempty = 0, tref = 0;
+    bool ragged = false;
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k)
-      if (k < nk)                                             // uniform
-        tiles += static_cast<uint32_t>(__builtin_amdgcn_readlane(
-            static_cast<int>(wave_incl_scan(seq_tiles(len_k[k], a.max_context))), 63));
+    for (int k = 0; k < KMAX; ++k) {
+      incl[k] = 0;
+      if (k < nk) {                                           // uniform
+        const uint32_t t = seq_tiles(len_k[k], a.max_context);
+        incl[k] = wave_incl_scan(t);
+        tiles += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[k]), 63));
+        const uint64_t some = __ballot(t > 0);
+        nonempty += static_cast<uint32_t>(__popcll(some));
+        if (tref == 0 && some != 0)
+          tref = static_cast<uint32_t>(
+              __builtin_amdgcn_readlane(static_cast<int>(t), static_cast<int>(__builtin_ctzll(some))));
+        ragged |= __any(t > 0 && t != tref);
+      }
+    }
     // Each row after a block's first costs the block its first loads and a
     // refill of its copy pipeline: a row is laid out as `cost` charged
     // positions then its n tiles, and blocks take equal shares of positions.
     // Charged only when every block's share exceeds `cost` positions (so every
-    // block holds a tile, and holds no row's charged positions alone).
-    cost = static_cast<uint64_t>(nhg) * tiles >= static_cast<uint64_t>(a.stream_row_cost + 1) * P
+    // block holds a tile, and holds no row's charged positions alone), and
+    // only when some row would start inside a block's share: equal rows whose
+    // count divides the blocks taking part start on share boundaries, each
+    // block then holds tiles of one row (split-K's partition of a uniform
+    // batch), and charges would only move the boundaries off the rows (config
+    // 2 through the stream schedule: 59.7 us with charges, 58.6 without).
+    const uint64_t T0 = static_cast<uint64_t>(nhg) * tiles;
+    const uint32_t rows = static_cast<uint32_t>(nhg) * nonempty;
+    const uint32_t Pe0 = static_cast<uint32_t>(min(static_cast<uint64_t>(P), T0));
+    const bool aligned = !ragged && rows > 0 && Pe0 % rows == 0;
+    cost = !aligned && T0 >= static_cast<uint64_t>(a.stream_row_cost + 1) * P
                ? static_cast<uint32_t>(a.stream_row_cost) : 0u;
-    // inclusive prefix sums of the sequences' positions
-    uint32_t incl[KMAX];
-    uint64_t total = 0;
+    // inclusive prefix sums of the sequences' positions (tiles plus charges)
+    uint64_t total = tiles;
+    if (cost != 0) {
+      total = 0;
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-      incl[k] = 0;
-      if (k < nk) {
-        const uint32_t t = seq_tiles(len_k[k], a.max_context);
-        incl[k] = wave_incl_scan(t > 0 ? t + cost : 0u);
-        total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[k]), 63));
+      for (int k = 0; k < KMAX; ++k) {
+        if (k < nk) {
+          const uint32_t t = seq_tiles(len_k[k], a.max_context);
+          incl[k] = wave_incl_scan(t > 0 ? t + cost : 0u);
+          total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[k]), 63));
+        }
       }
     }
     T = static_cast<uint64_t>(nhg) * total;
@@ -1462,7 +1517,7 @@ struct StreamStart {
     Pe = static_cast<int>(min(static_cast<uint64_t>(P), T));
     *f0 = *f1 = 0;
     if (b >= Pe) return;
-    const uint64_t f = static_cast<uint64_t>(b) * T / Pe;
+    const uint64_t f = share_bound(static_cast<uint32_t>(b), T, static_cast<uint32_t>(Pe));
     // the chunk holding f, then the lane within it
     uint64_t acc = 0;
     int kstar = 0;
@@ -1495,7 +1550,7 @@ struct StreamStart {
             (acc + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ik), c)) -
              (n + cost));
     *f0 = f;
-    *f1 = static_cast<uint64_t>(b + 1) * T / Pe;
+    *f1 = share_bound(static_cast<uint32_t>(b + 1), T, static_cast<uint32_t>(Pe));
   }
 };
 
@@ -1764,7 +1819,8 @@ __device__ __forceinline__ void coop_kernel_body(
       const int nhg = a.num_kv_heads / L::kHeads;
       const int HG = L::kHeads * a.group;
       const uint32_t nv = U.n + U.cost;                     // a row's positions
-      const int hg = static_cast<int>((U.f - U.sbase) / nv);
+      // (a sequence's rows span nhg * nv < 2^32 positions)
+      const int hg = static_cast<int>(static_cast<uint32_t>(U.f - U.sbase) / nv);
       if (hg >= nhg) break;                                   // (cannot happen)
       const uint64_t srow = U.sbase + static_cast<uint64_t>(hg) * nv;
       const uint64_t r0 = srow + U.cost;                      // the row's first tile
@@ -1783,7 +1839,7 @@ __device__ __forceinline__ void coop_kernel_body(
         const int j = threadIdx.x;
         int32_t* rec = a.row_meta + 2 * (static_cast<int64_t>(U.s) * a.num_q_heads + hg * HG + j);
         rec[0] = (b + row) * HG + j;
-        rec[1] = static_cast<int>((tl * U.Pe + U.Pe - 1) / U.T) - b + 1;
+        rec[1] = block_of_position(tl, U.T, static_cast<uint32_t>(U.Pe)) - b + 1;
       }
       {
         StreamWalk N = U;

@@ -4,7 +4,9 @@ The cooperative decode kernel's stream schedule (split_tokens = 0) lays all
 (sequence, group of 8 kv heads) rows end to end, each row as `cost` charged
 positions (no work) then its 32-token tiles, and gives block b < Pe =
 min(P, T) the positions [b T / Pe, (b + 1) T / Pe).  Charges apply only when
-the batch has at least (cost + 1) P tiles.  A block writes one partial per row
+the batch has at least (cost + 1) P tiles, and not when every non-empty row
+has the same tile count and the rows divide the blocks taking part (the rows
+then start on share boundaries: split-K's partition of a uniform batch).  A block writes one partial per row
 it holds tiles of, at entry (b + row) * HG + head; the block holding a row's
 first tile records the row's first entry and its block count, computed as
 (last tile's block) - b + 1 with the last tile's block
@@ -30,7 +32,9 @@ COST = 6          # the library's charge (tiles) per row a block starts mid-shar
 def _partition(lens, max_context, nhg, P, cost_param=COST, always_charge=False):
     n = [(max(0, min(x, max_context)) + 31) // 32 for x in lens]
     tiles = nhg * sum(n)
-    cost = cost_param if always_charge or tiles >= (cost_param + 1) * P else 0
+    ne = [x for x in n if x > 0]
+    aligned = len(set(ne)) == 1 and min(P, tiles) % (nhg * len(ne)) == 0
+    cost = cost_param if always_charge or (not aligned and tiles >= (cost_param + 1) * P) else 0
     rows = []                        # (seq, hg, first position, n)
     pos = 0
     for s, ns in enumerate(n):
@@ -155,4 +159,70 @@ def test_partition_limits():
     assert cost == COST and T < 2 ** 31
     assert _check([1, 17, 0, 33], 2048, 1, 256, 4) == 0
     assert _check([0, 0], 2048, 1, 256, 4) == 0
-    assert _check([5000], 8192, 2, 8, 5) == COST
+    # one sequence's two equal rows over 8 blocks: aligned, uncharged
+    assert _check([5000], 8192, 2, 8, 5) == 0
+    assert _check([5000, 3000], 8192, 2, 8, 5) == COST
+
+
+def test_uniform_batches_get_split_k_partition():
+    """Equal rows whose count divides the blocks: no charges, and block b
+    holds tiles [b k, (b + 1) k) of row b // (blocks per row), which is
+    split-K's partition (config 2: 8 rows of 1024 tiles over 256 blocks, 32
+    tiles each; config 8: 16 rows).  Equal rows that do not divide the
+    blocks (3 rows over 256) or unequal rows keep the charges.  (Shares within
+    a row may differ by a tile, as split-K's splits do at the row's end.)"""
+    for S, T, nhg in ((8, 32768, 1), (16, 32768, 1), (4, 32768, 2), (1, 393216, 1),
+                      (64, 16384, 1), (32, 65536 + 32, 1)):
+        rows, Tp, Pe, cost = _partition([T] * S, T, nhg, 256)
+        assert cost == 0, (S, T)
+        bpr = Pe // len(rows)                           # blocks per row
+        for b in range(Pe):
+            f, fe = b * Tp // Pe, (b + 1) * Tp // Pe
+            held = [r for r, (_, _, st, ns) in enumerate(rows) if max(f, st) < min(fe, st + ns)]
+            assert held == [b // bpr]
+        _check([T] * S, T, nhg, 256, 4)
+    assert _partition([65536] * 3, 65536, 1, 256)[3] == COST
+    assert _partition([16384] * 63 + [16000], 16384, 1, 256)[3] == COST
+
+
+def _share_bound(x, T, Pe):
+    """The kernel's floor(x T / Pe) (x <= Pe <= 2^16): T = q Pe + r, then
+    x q + floor(x r / Pe) with x r in 32 bits."""
+    q, r = T // Pe, T % Pe
+    xr = (x * r) & 0xFFFFFFFF
+    assert xr == x * r                                  # fits the kernel's 32 bits
+    return x * q + xr // Pe
+
+
+def _block_of_position(t, T, Pe):
+    """The kernel's floor((t Pe + Pe - 1) / T): an fp64 quotient when T < 2^32."""
+    num = t * Pe + Pe - 1
+    if T < 2 ** 32:
+        return int(np.floor(np.float64(num) / np.float64(T)))
+    return num // T
+
+
+def test_stream_start_arithmetic_is_exact():
+    """The stream schedule's share bounds and record counts use 32-bit and
+    fp64 divisions in place of 64-bit ones; both equal exact integer
+    arithmetic over random and boundary values (T up to 2^40, Pe up to
+    1024), and the fp64 path is the one taken for T < 2^32."""
+    g = np.random.default_rng(7)
+    cases = []
+    for _ in range(20000):
+        Pe = int(g.choice([1, 7, 255, 256, 1024]))
+        T = int(g.choice([Pe, Pe + 1, 2 ** 31 - 1, 2 ** 32 - 1, 2 ** 32 + 5, 2 ** 40 - 3,
+                          int(g.integers(Pe, 2 ** 33))]))
+        cases.append((Pe, T))
+    for Pe, T in cases:
+        for x in (0, 1, Pe - 1, Pe, int(g.integers(0, Pe + 1))):
+            assert _share_bound(x, T, Pe) == x * T // Pe
+        for t in (0, T - 1, T // 2, int(g.integers(0, T))):
+            b = _block_of_position(t, T, Pe)
+            assert b == (t * Pe + Pe - 1) // T
+            assert b * T // Pe <= t < (b + 1) * T // Pe       # the block holding t
+    # planted mistakes fail these checks: the share bound without its
+    # remainder term, and the record's block without the round-up
+    assert any(x * (T // Pe) != x * T // Pe for Pe, T in cases[:200] for x in (Pe - 1,))
+    assert any((t * Pe) // T != (t * Pe + Pe - 1) // T
+               for Pe, T in cases[:200] for t in (T - 1, T // 3) if Pe > 1)
