@@ -20,13 +20,10 @@
   fp16 partial alone, the drop-in call path -- timed in ``--rounds``
   interleaved rounds of K launches each, with HIP events on the launch
   stream.  Each figure is the median of the rounds' averages, with its range.
-  A leg of marked steps (an event after each kernel) times the partial and
-  the merge where they run inside a decode step; ``consistency`` checks that
-  they add up to the step within 1 us, reports how much faster the partial
-  runs between merges than back to back (``roofline`` keeps the slower,
-  back-to-back figure; ``frac_in_step`` is the other), and lists legs whose
-  rounds spread by more than 3 %.  (The merge-only leg is bound by the
-  host's launch rate: back-to-back merges run faster than the host launches them.)
+  The merge leg replays a HIP graph of 20 merges (launched one by one from
+  Python, merges run faster than the host launches them; that leg is
+  reported too).  ``consistency`` checks that step - partial equals the
+  merge within 1 us and lists legs whose rounds spread by more than 3 %.
 * ``value`` is whole-step HBM throughput: algorithmic bytes per step divided
   by the step time.  Algorithmic bytes count each packed KV byte once, plus
   the scales/zeros, q, out, block table and seq_lens.
@@ -506,25 +503,6 @@ def time_leg(go, steps, i0=0):
     return a.elapsed_time(b) * 1e3 / steps
 
 
-def time_marked_steps(go_partial, go_merge, steps, i0=0):
-    """Steps of partial + merge with an event after each kernel: (us per
-    step, us of the partial inside a step, us of the merge inside a step),
-    averaged over `steps`.  The partial is timed where it runs in a decode
-    step, between merges, rather than back to back with itself."""
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps + 1)]
-    torch.cuda.synchronize()
-    ev[0].record()
-    for i in range(steps):
-        go_partial(i0 + i)
-        ev[2 * i + 1].record()
-        go_merge(i0 + i)
-        ev[2 * i + 2].record()
-    torch.cuda.synchronize()
-    part = sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)) * 1e3 / steps
-    merge = sum(ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(steps)) * 1e3 / steps
-    return ev[0].elapsed_time(ev[2 * steps]) * 1e3 / steps, part, merge
-
-
 def prewarm(go, min_ms):
     """Launch go until at least `min_ms` of wall time has passed (in batches
     of 10, synchronised): a few ms into a run the decode runs up to 15 %
@@ -541,17 +519,12 @@ def prewarm(go, min_ms):
             return {"launches": n, "ms": round(el, 1)}
 
 
-def interleaved(legs, steps, rounds, settle=2, marked=None):
+def interleaved(legs, steps, rounds, settle=2):
     """Time every leg in `rounds` rounds, the legs one after another in each
     round (`settle` untimed calls before each timed run of `steps`), so that
-    all legs see the same phases of the GPU's clocks.  `marked` = (name,
-    partial go, merge go) adds a leg of marked steps (time_marked_steps),
-    recorded as name, name_partial and name_merge.  Returns {leg: [us per
+    all legs see the same phases of the GPU's clocks.  Returns {leg: [us per
     call of each round]}."""
     res = {k: [] for k in legs}
-    if marked is not None:
-        for k in ("", "_partial", "_merge"):
-            res[marked[0] + k] = []
     i = 0
     for _ in range(rounds):
         for name, go in legs.items():
@@ -560,18 +533,22 @@ def interleaved(legs, steps, rounds, settle=2, marked=None):
                 i += 1
             res[name].append(time_leg(go, steps, i))
             i += steps
-        if marked is not None:
-            name, gp, gm = marked
-            for _ in range(settle):
-                gp(i)
-                gm(i)
-                i += 1
-            st, pa, me = time_marked_steps(gp, gm, steps, i)
-            i += steps
-            res[name].append(st)
-            res[name + "_partial"].append(pa)
-            res[name + "_merge"].append(me)
     return res
+
+
+def graph_of(make_go, calls):
+    """`calls` launches of the launcher make_go() builds (on the capture
+    stream), captured in one HIP graph: back-to-back kernels that short,
+    launched one by one from Python, run faster than the host launches
+    them.  Returns go(i) replaying the graph, `calls` and the graph."""
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        go = make_go()
+        for i in range(calls):
+            go(i)
+    torch.cuda.synchronize()
+    return (lambda i: g.replay()), calls, g
 
 
 def summary(xs):
@@ -808,7 +785,9 @@ def main(argv=None):
     legs = {"int4_step": launcher(split)}
     time_leg(legs["int4_step"], max(args.warmup, 1))        # W untimed warm-up steps
     legs["int4_partial"] = launcher(split, "partial")
-    legs["merge"] = launcher(split, "merge")
+    mgo, mcalls, mgraph = graph_of(lambda: launcher(split, "merge"), 20)
+    legs["merge_graph_x%d" % mcalls] = mgo
+    legs["merge_host_launched"] = launcher(split, "merge")
     if fused is not None:
         legs["int4_step_separate_append"] = launcher(split, "step_sep")
     if fcopies is not None:
@@ -817,11 +796,9 @@ def main(argv=None):
                                              out, mode="partial")
     if not args.no_dropin:
         legs["dropin_graph_x%d" % dn] = dgo
-    # the step with an event after each kernel (config 5: its fused append
-    # stays in the step leg; the marked partial has none)
-    marked = None if fused is not None else ("int4_step_marked", legs["int4_partial"],
-                                             legs["merge"])
-    rounds = interleaved(legs, args.steps, args.rounds, marked=marked)
+    rounds = interleaved(legs, args.steps, args.rounds)
+    rounds["merge"] = [t / mcalls for t in rounds.pop("merge_graph_x%d" % mcalls)]
+    del mgraph
     if not args.no_dropin:
         rounds["dropin_graph"] = [t / dn for t in rounds.pop("dropin_graph_x%d" % dn)]
     # the merge leg ran after the partial leg of its round: both see the same
@@ -923,28 +900,22 @@ def main(argv=None):
     step_gbs = alg / (us_step * 1e-6) / 1e9
     part_gbs = alg_partial / (us_part * 1e-6) / 1e9
     traffic, traffic_note = measured_traffic(c)
-    # Consistency of the timed phases.  The merge leg (merges back to back)
-    # is bound by the host's launch rate, not the merge; the marked steps
-    # time the partial and the merge where they run in a decode step, and
-    # must add up to the unmarked step.  The partial runs a little faster
-    # between merges than back to back (the partial leg), so step - partial
-    # leg understates the merge; both are reported.
+    # Consistency of the timed phases: the step is the partial plus the
+    # merge.  The merge leg is a graph of back-to-back merges (launched one
+    # by one from Python they run faster than the host launches them: the
+    # host-launched leg is reported for that).  The partial runs a little
+    # faster between merges, inside steps, than back to back (kernel
+    # traces), so step - partial can fall short of the merge.
+    gap = us_step - us_part - us_merge
     flagged = sorted(k for k, v in S.items() if v["spread"] is not None and v["spread"] > 0.03)
-    checks = {"step_minus_partial_us": round(us_step - us_part, 2),
-              "merge_leg_us": us_merge,
+    checks = {"step_minus_partial_us": round(us_step - us_part, 2), "merge_us": us_merge,
+              "merge_host_launched_us": S["merge_host_launched"]["median"],
+              "step_minus_partial_minus_merge_us": round(gap, 2),
+              "step_equals_partial_plus_merge": abs(gap) <= 1.0,
               "legs_with_round_spread_over_3pct": flagged}
-    if "int4_step_marked" in S:
-        mp, mm = S["int4_step_marked_partial"]["median"], S["int4_step_marked_merge"]["median"]
-        checks.update({
-            "partial_in_step_us": mp, "merge_in_step_us": mm,
-            "marked_step_us": S["int4_step_marked"]["median"],
-            "step_minus_partial_in_step_us": round(us_step - mp, 2),
-            "step_minus_partial_in_step_minus_merge_in_step_us": round(us_step - mp - mm, 2),
-            "step_equals_partial_plus_merge": abs(us_step - mp - mm) <= 1.0,
-            "partial_leg_minus_partial_in_step_us": round(us_part - mp, 2)})
-    else:
+    if fused is not None:
         checks["note"] = ("config 5's step appends the new token inside the partial launch, "
-                          "the partial leg does not; no marked steps")
+                          "the partial leg does not")
     rec = {
         "metric": "decode-attn us/step and achieved HBM GB/s (% of peak), INT4 vs fp16 KV",
         "value": round(step_gbs, 1),
@@ -990,10 +961,6 @@ def main(argv=None):
                      "algorithmic_bytes_per_launch": alg_partial,
                      "avg_launch_us": us_part,
                      "avg_launch_us_range": [S["int4_partial"]["min"], S["int4_partial"]["max"]],
-                     **({"avg_launch_us_in_step": S["int4_step_marked_partial"]["median"],
-                         "frac_in_step": round(alg_partial / (S["int4_step_marked_partial"]["median"]
-                                                              * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-                        if "int4_step_marked_partial" in S else {}),
                      "stream_ceiling_frac": round(stream["frac_of_peak"], 4),
                      "frac_of_stream_ceiling": round(part_gbs / stream["GBs"], 4)},
         "legs_us": S,

@@ -1571,13 +1571,337 @@ struct StreamStart {
 // its first entry and the count of blocks holding the row's tiles for the
 // merge.
 
+// ---------------------------------------------------------------------------
+// Wide query groups: 5 <= G <= 8 query heads per kv head over INT8 K with one
+// scale per row and packed INT4 V at D = 128 (config 5: G = 5, V g32).  With
+// rows (head, V group) these shapes need two head sets of 16 rows (20 rows
+// at G = 5, the second set using 4 of its 16) and 32 PV products per tile.
+// Here one set serves every head:
+//  QK  rows r = 2 g + dup, both rows of head g carrying all of q (one K scale
+//      per token, so no row needs a part of q): the output lane (token col,
+//      blk) holds heads 2 blk and 2 blk + 1 in its rows 0 and 2.
+//  PV  products by 32-column blocks m and nibble h: lane col of product
+//      (m, h) is column 32 m + 2 col + h (nibble h of byte 16 m + col), so
+//      every product lies inside V group vg(m), and its A operand A_vg has
+//      rows (g, hi / lo) of P' = p s_v[vg]: a lane's (head 2 blk, head
+//      2 blk + 1) x (hi, lo) are the slots 0-3 of one identity transpose,
+//      whose output row is 2 g + hl.  8 PV products and 8 transposes per
+//      tile whatever G (two head sets: 32 products, or 16 with group pairs).
+//  V   read from LDS as byte pairs: byte 16 m + col of two tokens in the two
+//      halves of a dword, one mask per nibble (kNib1 / kNib16).
+// ---------------------------------------------------------------------------
+template <int NGV, bool VASYM>
+struct WaveStateW {
+  static constexpr int NCH = 4;                 // D = 128
+  static constexpr int GPL = 2;                 // heads per lane
+  using ST = SubTile<4, NGV, 8, 1, 4>;          // INT8 K, one scale per row
+  h8 aq[NCH];          // q rows 2g, 2g + 1 = head g (A operands of QK)
+  f4 cinit;            // QK accumulator start: -128 * 2^-24 * sum(q) (biased codes)
+  h4 eye;              // identity, B operand of the P' transposes
+  f4 acc[4][2];        // [column block m][nibble h]: rows (g, hi/lo)
+  float m_run[GPL], lsum[GPL], sl2[GPL], thr[GPL];
+  float zacc[GPL][NGV];
+  float kexp, svlim;
+
+  __device__ static constexpr int vg_of(int m) { return m * NGV / 4; }
+
+  template <bool MASK>
+  __device__ __forceinline__ void scores(const ST (&st)[2], const bool (&valid)[2],
+                                         float (&score)[2][GPL]) const {
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      f4 S = cinit;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            aq[c], bytes_to_h8_sub(st[x].k.dw(2 * c), st[x].k.dw(2 * c + 1)), S, 0, 0, 0);
+      const float sk = st[x].ks.get(0);
+#pragma unroll
+      for (int gi = 0; gi < GPL; ++gi)
+        score[x][gi] = (MASK && !valid[x]) ? -INFINITY : sk * S[2 * gi];
+    }
+  }
+
+  // V scales in fp16 (0 past the end) and their largest value.
+  template <bool MASK>
+  __device__ __forceinline__ float vscales(const ST (&st)[2], const bool (&valid)[2],
+                                           _Float16 (&sv)[2][NGV]) const {
+    float m = 0.0f;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int g = 0; g < NGV; ++g) {
+        sv[x][g] = st[x].vs.geth(g);
+        if constexpr (MASK) sv[x][g] = valid[x] ? sv[x][g] : static_cast<_Float16>(0.0f);
+        m = fmaxf(m, static_cast<float>(sv[x][g]));
+      }
+    return m;
+  }
+
+  __device__ __forceinline__ bool slow_tile(const float (&score)[2][GPL], float svmax) const {
+    bool up = svmax > svlim;
+#pragma unroll
+    for (int gi = 0; gi < GPL; ++gi) up |= fmaxf(score[0][gi], score[1][gi]) > m_run[gi] + thr[gi];
+    return __any(up);
+  }
+
+  // As WaveState::slow_step: raise the running maxima that moved, lower k
+  // for a larger V scale, rescale by both (powers of two for k).
+  __device__ __forceinline__ void slow_step(const float (&score)[2][GPL], float svmax) {
+    float smax = row_max16(svmax);
+    smax = fmaxf(smax, __shfl_xor(smax, 16, kWave));
+    smax = fmaxf(smax, __shfl_xor(smax, 32, kWave));
+    int e = 0;
+    frexpf(smax, &e);
+    const float knew = fminf(kexp, static_cast<float>(12 - e));
+    const float kscale = ldexpf(1.0f, static_cast<int>(knew - kexp));
+    kexp = knew;
+    svlim = ldexpf(1.0f, 12 - static_cast<int>(knew));
+    float alpha[GPL];
+#pragma unroll
+    for (int gi = 0; gi < GPL; ++gi) {
+      const float tmax = row_max16(fmaxf(score[0][gi], score[1][gi]));
+      const bool up = tmax > m_run[gi] + thr[gi];
+      alpha[gi] = (up ? __builtin_amdgcn_exp2f((m_run[gi] - tmax) * sl2[gi]) : 1.0f) * kscale;
+      m_run[gi] = up ? tmax : m_run[gi];
+    }
+#pragma unroll
+    for (int gi = 0; gi < GPL; ++gi) {
+      lsum[gi] *= alpha[gi];
+#pragma unroll
+      for (int g = 0; g < NGV; ++g) zacc[gi][g] *= alpha[gi];
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[m][h][i] *= alpha[i / 2];
+  }
+
+  // p (times 2^k), P' = p s_v[vg] as fp16 hi + lo, the zero-point term, and
+  // for each V group the PV A operand (rows 2g + hl, slots = tokens).
+  template <bool MASK>
+  __device__ __forceinline__ void probs(const ST (&st)[2], const bool (&valid)[2],
+                                        const float (&score)[2][GPL],
+                                        const _Float16 (&svt)[2][NGV], h8 (&aw)[NGV]) {
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      float p[GPL];
+#pragma unroll
+      for (int gi = 0; gi < GPL; ++gi) {
+        p[gi] = __builtin_amdgcn_exp2f(fmaf(score[x][gi] - m_run[gi], sl2[gi], kexp));
+        lsum[gi] += p[gi];
+      }
+#pragma unroll
+      for (int g = 0; g < NGV; ++g) {
+        const float sv = static_cast<float>(svt[x][g]);
+        const float P0 = fmaf(p[0], sv, 0.0f), P1 = fmaf(p[1], sv, 0.0f);
+        if constexpr (VASYM) {
+          float zv = st[x].vz.get(g);
+          if constexpr (MASK) zv = valid[x] ? zv : 0.0f;
+          zacc[0][g] = fmaf(p[0], zv, zacc[0][g]);
+          zacc[1][g] = fmaf(p[1], zv, zacc[1][g]);
+        } else {
+          zacc[0][g] = fmaf(-8.0f, P0, zacc[0][g]);
+          zacc[1][g] = fmaf(-8.0f, P1, zacc[1][g]);
+        }
+        const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(P0, P1));
+        const float r0 = fmaf(p[0], sv, -static_cast<float>(hi[0]));
+        const float r1 = fmaf(p[1], sv, -static_cast<float>(hi[1]));
+        const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+        // slots 0-3: (head 2 blk, hi), (2 blk, lo), (2 blk + 1, hi), (2 blk + 1, lo)
+        const h4 xin = {hi[0], lo[0], hi[1], lo[1]};
+        const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+        const f4 t = __builtin_amdgcn_mfma_f32_16x16x16f16(xin, eye, zero4, 0, 0, 0);
+        const h2 t01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(t[0], t[1]));
+        const h2 t23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(t[2], t[3]));
+        aw[g][4 * x + 0] = t01[0]; aw[g][4 * x + 1] = t01[1];
+        aw[g][4 * x + 2] = t23[0]; aw[g][4 * x + 3] = t23[1];
+      }
+    }
+  }
+
+  // PV: vb[m][q] holds byte 16 m + col of tokens (t0, t0 + 1) in its two
+  // halves, t0 = 16 (q / 2) + 4 blk + 2 (q % 2): the tokens of A slots 2q,
+  // 2q + 1.  Nibble h of those bytes is column 32 m + 2 col + h.
+  __device__ __forceinline__ void pv(const uint32_t (&vb)[4][4], const h8 (&aw)[NGV]) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u4 bw;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bw[q] = vb[m][q] & (h ? kNib16 : kNib1);
+        acc[m][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[vg_of(m)],
+                                                           __builtin_bit_cast(h8, bw), acc[m][h],
+                                                           0, 0, 0);
+      }
+  }
+};
+
+// q rows (two per head), constants and accumulators of the wave serving kv
+// head `kvh` with all its G <= 8 query heads (qw from load_q<128, 2>: lane
+// (col, blk) holds elements 32 blk .. 32 blk + 31 of head col / 2).
+template <int NGV, bool VASYM>
+__device__ __forceinline__ void init_wave_w(WaveStateW<NGV, VASYM>& W, const uint4 (&qw)[4],
+                                            const DecodeArgs& a, int col, int blk) {
+  const bool qneg = a.scale_log2 < 0.0f;
+  const bool qzero = a.scale_log2 == 0.0f;
+  const bool on = col < 2 * a.group && !qzero;
+  uint16_t qv[32];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t ws[4] = {qw[i].x, qw[i].y, qw[i].z, qw[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qv[8 * i + 2 * j] = static_cast<uint16_t>(ws[j]);
+      qv[8 * i + 2 * j + 1] = static_cast<uint16_t>(ws[j] >> 16);
+    }
+  }
+  float qscale = 1.0f;
+  if (a.q_bf16) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(bf16_bits_to_float(qv[i])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    int ex = 0;
+    frexpf(mx, &ex);
+    qscale = mx > 0.0f ? ldexpf(1.0f, 14 - ex) : 1.0f;
+  }
+  float qpart = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int el = 8 * c + kByteK8[e];
+      _Float16 v = !on ? _Float16(0)
+                   : a.q_bf16 ? static_cast<_Float16>(bf16_bits_to_float(qv[el]) * qscale)
+                              : __builtin_bit_cast(_Float16, qv[el]);
+      if (qneg) v = -v;
+      W.aq[c][e] = v;
+      qpart += static_cast<float>(v);
+    }
+  qpart += __shfl_xor(qpart, 16, kWave);
+  qpart += __shfl_xor(qpart, 32, kWave);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) W.cinit[i] = -128.0f * (__shfl(qpart, 4 * blk + i, kWave) * 0x1p-24f);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) W.eye[e] = (blk == col / 4 && e == col % 4) ? 1.0f : 0.0f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) W.acc[m][0] = W.acc[m][1] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    W.m_run[gi] = -INFINITY;
+    W.lsum[gi] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < NGV; ++g) W.zacc[gi][g] = 0.0f;
+    const float qs = __shfl(qscale, 4 * blk + 2 * gi, kWave);
+    W.sl2[gi] = (qzero ? 1.0f : fabsf(a.scale_log2)) * 0x1p24f / qs;
+    W.thr[gi] = kRescaleLog2 / W.sl2[gi];
+  }
+  W.kexp = 40.0f;
+  W.svlim = 0x1p-28f;
+}
+
+// The wave's partial (acc, max, sum) for each of its kv head's G query heads
+// at entry base + g * stride.
+template <int NGV, bool VASYM>
+__device__ __forceinline__ void write_partials_w(WaveStateW<NGV, VASYM>& W, const DecodeArgs& a,
+                                                 int64_t base, int64_t stride, int col, int blk) {
+  const int G = a.group;
+  const float kinv = ldexpf(1.0f, -static_cast<int>(W.kexp));
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    W.lsum[gi] = row_sum16(W.lsum[gi]) * kinv;
+#pragma unroll
+    for (int g = 0; g < NGV; ++g) W.zacc[gi][g] = row_sum16(W.zacc[gi][g]);
+  }
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    const int g = 2 * blk + gi;
+    if (g < G) {
+      const int64_t row = base + g * stride;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const f4 v = W.acc[m][h];
+          const float hl = gi ? v[2] + v[3] : v[0] + v[1];
+          // high nibbles arrive as 16 n: a factor 16 fewer
+          a.part_o[row * 128 + 32 * m + 2 * col + h] =
+              fmaf(hl, h ? 0x1p20f : 0x1p24f, W.zacc[gi][WaveStateW<NGV, VASYM>::vg_of(m)]) * kinv;
+        }
+      if (col == 0) {
+        a.part_ml[2 * row] = W.m_run[gi] * W.sl2[gi];
+        a.part_ml[2 * row + 1] = W.lsum[gi];
+      }
+    }
+  }
+}
+
+// V of this wave's head as byte pairs (WaveStateW::pv): vb[m][q] = byte
+// 16 m + col of tokens t0 and t0 + 1, t0 = 16 (q / 2) + 4 blk + 2 (q % 2).
+template <class L>
+__device__ __forceinline__ void coop_read_v_w(const uint8_t* buf, int wave, int col, int blk,
+                                              uint32_t (&vb)[4][4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint8_t* sub = buf + L::V_OFF + (q / 2) * 16 * L::CROWV;
+    const int r0 = 4 * blk + 2 * (q % 2);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int byte = wave * L::HBV + 16 * m + col;
+      const uint32_t b0 = sub[L::code_off(L::CROWV, r0, byte)];
+      const uint32_t b1 = sub[L::code_off(L::CROWV, r0 + 1, byte)];
+      vb[m][q] = b0 | (b1 << 16);
+    }
+  }
+}
+
+// One tile of the wide-group kernel, pipelined as coop_tile: copies of tile
+// i + NBUF - 1, this wave's slice of tile i, QK of tile i next to PV of tile
+// i - 1, tile i's V into the registers PV has consumed, then P' of tile i.
+template <class L, int NGV, bool VASYM, bool MASK, bool PV_PREV>
+__device__ __forceinline__ void coop_tile_w(WaveStateW<NGV, VASYM>& W, const CoopAddr& C, int i,
+                                            int ntiles, int t_begin, int t_end, int wave, int col,
+                                            int blk, const uint8_t* cur, uint8_t* nxt,
+                                            uint32_t (&vb)[4][4], h8 (&aw)[NGV], PageWindow& PW,
+                                            int lane) {
+  using WS = WaveStateW<NGV, VASYM>;
+  constexpr int NBUF = L::NBUF;
+  const int tb = t_begin + 32 * i;
+  if (i + NBUF - 1 < ntiles) coop_issue<L>(C, PW, lane, wave, tb + 32 * (NBUF - 1), t_end, nxt);
+  typename WS::ST st[2];
+  coop_read<L, false, VASYM>(cur, wave, col, blk, st);
+  bool valid[2] = {true, true};
+  if constexpr (MASK) {
+    valid[0] = tb + col < t_end;
+    valid[1] = tb + 16 + col < t_end;
+  }
+  float score[2][WS::GPL];
+  W.template scores<MASK>(st, valid, score);
+  if constexpr (PV_PREV) W.pv(vb, aw);
+  coop_read_v_w<L>(cur, wave, col, blk, vb);
+  _Float16 sv[2][NGV];
+  const float svmax = W.template vscales<MASK>(st, valid, sv);
+  if (W.slow_tile(score, svmax)) W.slow_step(score, svmax);
+  W.template probs<MASK>(st, valid, score, sv, aw);
+  wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
+  __syncthreads();
+}
+
 // One segment: tokens [t_begin, t_begin + seg_tokens) (cut at the sequence's
 // length) of sequence `seq`, kv heads 8 hg .. 8 hg + 7.  seq_len < 0: load it
 // here (together with q and the block table).  Partial of head set s, query
 // head g of this wave at entry base(s) + g * stride, base(s) = base0 +
 // s * heads_per_set.  Returns without work (uniformly) when the segment is
 // empty.
-template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8>
+// WIDE: the wide-group wave state (WaveStateW: one set for 5 <= G <= 8,
+// INT8 K with one scale per row, INT4 V with NG groups, D = 128).
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8,
+          bool WIDE = false>
 __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
                                              uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8>::NBUF]
                                                            [CoopLayout<D, NG, K8, NGK, V8>::BYTES],
@@ -1665,9 +1989,16 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
   // wait for these loads (whose counter the copies share) holds up the
   // copies in flight.
   const int seq_len_raw = seq_len_known >= 0 ? seq_len_known : a.seq_lens[seq];
+  static_assert(!WIDE || (D == 128 && K8 && NGK == 1 && !V8 && !KASYM && NSET == 1),
+                "the wide-group wave state's shapes");
   uint4 qw[NSET][D / 32];
+  if constexpr (WIDE) {
+    load_q<D, 2>(qw[0], a, seq, kvh, col, blk, 0);     // two rows per head, all of q
+  } else {
 #pragma unroll
-  for (int s = 0; s < NSET; ++s) load_q<D, NG>(qw[s], a, seq, kvh, col, blk, s * heads_per_set<NG>());
+    for (int s = 0; s < NSET; ++s)
+      load_q<D, NG>(qw[s], a, seq, kvh, col, blk, s * heads_per_set<NG>());
+  }
   PageWindow PW;
   PW.last = (a.max_context - 1) >> C.bs_shift;
   PW.fill(C.bt, lane, t_begin >> C.bs_shift);              // waits for all three
@@ -1685,6 +2016,31 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
 #pragma unroll
   for (int t = 0; t < NBUF - 1; ++t)
     if (t < ntiles) coop_issue<L>(C, PW, lane, wave, t_begin + 32 * t, t_end, lds[t]);
+  const int nfull = (t_end - t_begin) / 32;
+  if constexpr (WIDE) {
+    WaveStateW<NG, VASYM> W;
+    init_wave_w(W, qw[0], a, col, blk);
+    wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
+    __syncthreads();
+    uint32_t vb[4][4];
+    h8 aw[NG];
+#define KNLP_COOP_TILE_W(MASK, PV_PREV)                                                     \
+  coop_tile_w<L, NG, VASYM, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, col, blk, \
+                                           lds[i % NBUF], lds[(i + NBUF - 1) % NBUF], vb,   \
+                                           aw, PW, lane)
+    int i = 0;
+    if (nfull > 0) {
+      KNLP_COOP_TILE_W(false, false);
+      for (i = 1; i < nfull; ++i) KNLP_COOP_TILE_W(false, true);
+      if (i < ntiles) KNLP_COOP_TILE_W(true, true);
+    } else {
+      KNLP_COOP_TILE_W(true, false);
+    }
+#undef KNLP_COOP_TILE_W
+    W.pv(vb, aw);
+    write_partials_w(W, a, base0, stride, col, blk);
+    return;
+  }
   // q -> matrix-core operands while the first tiles are in flight
   WS W[NSET];
 #pragma unroll
@@ -1697,7 +2053,6 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
   // the PV of the last tile
   typename WS::VWord vw[2][4];
   h8 ahi[NSET], alo[NSET];
-  const int nfull = (t_end - t_begin) / 32;
 #define KNLP_COOP_TILE(MASK, PV_PREV)                                                       \
   coop_tile<L, D, NSET, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, col, blk,     \
                                        lds[i % NBUF], lds[(i + NBUF - 1) % NBUF], vw, ahi,  \
@@ -1774,7 +2129,8 @@ struct StreamWalk {
 // The two schedules are separate kernels (each with its own register
 // allocation: the stream loop's state would otherwise cost the split kernel
 // registers through its whole tile loop).
-template <bool STREAM, int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8>
+template <bool STREAM, int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8,
+          bool WIDE>
 __device__ __forceinline__ void coop_kernel_body(
     const DecodeArgs& a,
     uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8>::NBUF][CoopLayout<D, NG, K8, NGK, V8>::BYTES]) {
@@ -1786,7 +2142,7 @@ __device__ __forceinline__ void coop_kernel_body(
     const int seq = blockIdx.y;
     const int hg = blockIdx.z;
     const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + (hg * L::kHeads + wave) * a.group;
-    coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(
+    coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE>(
         a, lds, seq, hg, split * a.split_tokens, a.split_tokens, -1,
         row0 * a.num_splits + split, a.num_splits);
   } else {
@@ -1854,7 +2210,7 @@ __device__ __forceinline__ void coop_kernel_body(
       KArgs* kp = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
       asm volatile("" : "+s"(kp));
       const DecodeArgs& A = *(const DecodeArgs*)kp;
-      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(
+      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE>(
           A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
           static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
       StreamWalk V = StreamWalk::uniform(walk);
@@ -1877,20 +2233,22 @@ __device__ __forceinline__ void coop_kernel_body(
   }
 }
 
-template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false>
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false,
+          bool WIDE = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_mfma_coop_kernel(DecodeArgs a) {
   using L = CoopLayout<D, NG, K8, NGK, V8>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[L::NBUF][L::BYTES];
-  coop_kernel_body<false, D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(a, lds);
+  coop_kernel_body<false, D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE>(a, lds);
 }
 
-template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false>
+template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8 = false,
+          bool WIDE = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_mfma_coop_stream_kernel(DecodeArgs a) {
   using L = CoopLayout<D, NG, K8, NGK, V8>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[L::NBUF][L::BYTES];
-  coop_kernel_body<true, D, NG, KASYM, VASYM, K8, NGK, NSET, V8>(a, lds);
+  coop_kernel_body<true, D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE>(a, lds);
 }
 
 inline int heads_per_block_mfma(int num_kv_heads) {

@@ -52,6 +52,13 @@ int launch_coop(const DecodeArgs& a, int head_size, hipStream_t stream) {
     if (va) KNLP_LAUNCH_COOP(128, NG, false, true, true, NGK, 2);                         \
     else KNLP_LAUNCH_COOP(128, NG, false, false, true, NGK, 2);                           \
   }
+  // INT8 K with one scale per row, INT4 V in four groups, 5 <= G <= 8: the
+  // wide-group wave state (one head set; kv_decode_mfma.h, WaveStateW)
+  if (k8 && !v8 && head_size == 128 && ng == 4 && ngk == 1 && a.group >= 5 && a.group <= 8) {
+    if (va) KNLP_LAUNCH_COOP(128, 4, false, true, true, 1, 1, false, true);
+    else KNLP_LAUNCH_COOP(128, 4, false, false, true, 1, 1, false, true);
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
+  }
 #define KNLP_INT8K(NG)                                                                    \
   if (k8 && !v8 && head_size == 128 && ng == NG) {                                        \
     if (ngk == 1) {                                                                       \
