@@ -203,11 +203,17 @@ int32_t knlp_kv_decode_plan(int32_t num_seqs, int32_t num_kv_heads, int32_t num_
   // step at 64 tokens against 17 us at 256); partials cost (D+2)*4 bytes per
   // q head and split on each side of the merge, negligible at that size.
   const int g = num_q_heads / num_kv_heads;
-  const bool wide = num_kv_heads % 8 == 0 && k_format != KNLP_KV_FP16 &&
+  // the cooperative kernel takes 8 kv heads per block, or 4 with fp16 K (at
+  // D = 128)
+  const int coop_heads = k_format == KNLP_KV_FP16 ? 4 : 8;
+  const bool wide = num_kv_heads % coop_heads == 0 &&
+                    (k_format != KNLP_KV_FP16 ||
+                     (head_size == 128 &&
+                      (v_format == KNLP_KV_FP16 || (v_group_size > 0 && head_size / v_group_size >= 2)))) &&
                     mfma_supported(g, head_size, k_format,
                                    k_format == KNLP_KV_FP16 ? head_size : k_group_size, v_format,
                                    v_format == KNLP_KV_FP16 ? head_size : v_group_size, 0);
-  const int hpb = wide ? 8 : heads_per_block(num_kv_heads);
+  const int hpb = wide ? coop_heads : heads_per_block(num_kv_heads);
   const int64_t hgroups = (num_kv_heads + hpb - 1) / hpb;
   const int64_t target = (wide ? 1LL : 2LL) * num_cus();
   // tokens over all sequences: the caller's host-side total when it has one

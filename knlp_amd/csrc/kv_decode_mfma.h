@@ -363,7 +363,10 @@ struct WaveState {
   static constexpr int NGV = NG;       // V scale groups per token
   // V codes: packed INT4 (one dword of 8 nibble-columns per token and lane in
   // pv_columns) or INT8 (V8: 8 bytes)
-  using VWord = typename std::conditional<V8, uint2, uint32_t>::type;
+  // fp16 V (V16, cooperative kernel): 16 bytes, the 8 halves of columns
+  // 8 col .. 8 col + 7 of one token (D = 128)
+  using VWord = typename std::conditional<V16, uint4,
+                                          typename std::conditional<V8, uint2, uint32_t>::type>::type;
   // INT8 K codes: two dwords per QK chunk, one scale per NG / NGK row groups
   static constexpr bool K8 = KCH == 2 * NCH;
   // fp16 K: four dwords of halves per QK chunk, used as they are (no scale)
@@ -693,6 +696,34 @@ struct WaveState {
           acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
           acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
         }
+      }
+    }
+  }
+
+  // PV with fp16 V rows read from LDS (cooperative kernel): vw[x][i] holds
+  // the halves of columns (D/16) col .. (D/16) col + 7 of token 16x + 4blk + i
+  // (rows past the end read as 0), the tokens of this lane's A slots 4x + i;
+  // accumulator j = 2c + h holds column (D/16) col + j, whose B operand takes
+  // half j of each token, two tokens per dword with one v_perm (as pv_rows16).
+  __device__ __forceinline__ void pv_columns(const uint4 (&vw)[2][4], const h8& ahi,
+                                             const h8& alo) {
+    const auto dw = [](const uint4& u, int w) {
+      return w == 0 ? u.x : w == 1 ? u.y : w == 2 ? u.z : u.w;
+    };
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * c + h;
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        u4 bw;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bw[q] = __builtin_amdgcn_perm(dw(vw[q / 2][2 * (q % 2) + 1], j >> 1),
+                                        dw(vw[q / 2][2 * (q % 2)], j >> 1), sel);
+        const h8 bv = __builtin_bit_cast(h8, bw);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv, acc[c][h], 0, 0, 0);
+        acc[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv, acc[c][h], 0, 0, 0);
       }
     }
   }
@@ -1100,23 +1131,28 @@ __global__ __launch_bounds__(V16 ? 256 : 512) void decode_mfma_kernel(DecodeArgs
 // staged tile and, after common-subexpression elimination, its K and V
 // conversions.
 // ---------------------------------------------------------------------------
-template <int D, int NG, bool K8 = false, int NGK = NG, bool V8 = false>
+template <int D, int NG, bool K8 = false, int NGK = NG, bool V8 = false, bool K16 = false,
+          bool V16 = false>
 struct CoopLayout {
-  static constexpr int kHeads = 8;
-  static constexpr int HBK = K8 ? D : D / 2;       // K code bytes per head and token
-  static constexpr int HBV = V8 ? D : D / 2;       // V code bytes per head and token
-  static constexpr int SBK = 2 * NGK;              // K scale bytes per head and token
-  static constexpr int SBV = 2 * NG;               // V scale bytes per head and token
+  // fp16 K rows (512 bytes per token and kv head with fp16 V) take 4 kv heads
+  // per block, so that 32-token tiles of K and V (64 KB) double-buffer in
+  // LDS; packed rows take 8
+  static constexpr int kHeads = K16 ? 4 : 8;
+  static constexpr int WPS = kHeads / 2;           // waves copying each sub-tile
+  static constexpr int HBK = K16 ? 2 * D : K8 ? D : D / 2;   // K bytes per head and token
+  static constexpr int HBV = V16 ? 2 * D : V8 ? D : D / 2;   // V bytes per head and token
+  static constexpr int SBK = K16 ? 0 : 2 * NGK;    // K scale bytes per head and token
+  static constexpr int SBV = V16 ? 0 : 2 * NG;     // V scale bytes per head and token
   static constexpr int CROWK = kHeads * HBK;       // LDS rows (16 rows per sub-tile)
   static constexpr int CROWV = kHeads * HBV;
   static constexpr int SROWK = kHeads * SBK;
   static constexpr int SROWV = kHeads * SBV;
   static constexpr int CPSK = 16 * CROWK / 1024;   // 1-KB wave copies per code sub-tile
   static constexpr int CPSV = 16 * CROWV / 1024;
-  static constexpr int NPWK = CPSK / 4;            // code parts per wave and tile (4 waves
-  static constexpr int NPWV = CPSV / 4;            // per sub-tile)
+  static constexpr int NPWK = CPSK / WPS;          // code parts per wave and tile
+  static constexpr int NPWV = CPSV / WPS;
   static constexpr int NJ = NPWK + NPWV;           // code copies per wave and tile
-  static constexpr bool HAS_KZ = !K8;              // K zero-points (asymmetric INT4 K)
+  static constexpr bool HAS_KZ = !K8 && !K16;      // K zero-points (asymmetric INT4 K)
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = K_OFF + 2 * 16 * CROWK;
   static constexpr int KS_OFF = V_OFF + 2 * 16 * CROWV;   // scale arrays, 2 sub-tiles each
@@ -1127,9 +1163,19 @@ struct CoopLayout {
   // LDS tile buffers at one block per CU (160 KB): copies run NBUF - 1 tiles ahead
   static constexpr int NBUF = 4 * BYTES <= 160 * 1024 ? 4 : 3 * BYTES <= 160 * 1024 ? 3 : 2;
   static_assert(NBUF * BYTES <= 160 * 1024, "tile buffers fit one CU's LDS");
-  static_assert(CPSK % 4 == 0 && CPSV % 4 == 0 && NPWK >= 1 && NPWK <= 4 && NPWV <= 4,
-                "each sub-tile's code parts split evenly over its 4 waves");
+  static_assert(CPSK % WPS == 0 && CPSV % WPS == 0 && NPWK >= 1 && NPWK <= 8 && NPWV >= 1 &&
+                    NPWV <= 8,
+                "each sub-tile's code parts split evenly over its waves");
   static_assert(16 * SROWK <= 1024 && 16 * SROWV <= 1024, "one wave copy per scale sub-tile");
+  // a lane copies one 16-byte chunk of one scale row (the block's heads'
+  // scales of one token), so rows must be whole chunks
+  static_assert(SROWK % 16 == 0 && SROWV % 16 == 0, "scale rows of whole 16-byte chunks");
+  // The scale array wave w copies (of its sub-tile w % 2): 8 waves take
+  // array w / 2 (0 K scales, 1 V scales, 2 K zeros, 3 V zeros); with fp16 K
+  // (no K scales or zeros) 4 waves take V scales (w / 2 = 0) and V zeros.
+  __host__ __device__ static constexpr int s_array(int wave) {
+    return kHeads == 8 ? wave >> 1 : ((wave >> 1) == 0 ? 1 : 3);
+  }
   // scale array a: 0 K scales, 1 V scales, 2 K zeros, 3 V zeros
   __host__ __device__ static constexpr int s_off(int a) {
     return a == 0 ? KS_OFF : a == 1 ? VS_OFF : a == 2 ? KZ_OFF : VZ_OFF;
@@ -1161,7 +1207,7 @@ struct CoopAddr {
   const uint8_t* vc;
   const uint8_t* sp;      // this wave's scale array, head h0
   uint32_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
-  uint32_t lk[4], lv[4], ls;   // lane byte offsets in HBM (code parts, scale chunk)
+  uint32_t lk[8], lv[8], ls;   // lane byte offsets in HBM (code parts, scale chunk)
   bool same_kv;           // K and V codes share their strides (one page offset)
   bool s_arr_on;          // this wave copies a scale array (wave-uniform)
   bool s_on;              // this lane copies a scale chunk
@@ -1217,13 +1263,14 @@ __device__ __forceinline__ void coop_issue(const CoopAddr& C, PageWindow& PW, in
   const uint32_t of = static_cast<uint32_t>(pb & ((1 << C.bs_shift) - 1));
   const uint64_t ok = static_cast<uint64_t>(pg) * C.kc_b + of * C.kc_p;
   const uint64_t ov = C.same_kv ? ok : static_cast<uint64_t>(pg) * C.vc_b + of * C.vc_p;
+  // this wave's parts (wave >> 1) + WPS k of each code sub-tile
   const int p0 = (wave >> 1) * 1024;
   uint8_t* dk = buf + L::K_OFF + C.x * 16 * L::CROWK + p0;
   uint8_t* dv = buf + L::V_OFF + C.x * 16 * L::CROWV + p0;
 #pragma unroll
-  for (int k = 0; k < L::NPWK; ++k) lds_copy16(C.kc + ok, C.lk[k], dk + k * 4096);
+  for (int k = 0; k < L::NPWK; ++k) lds_copy16(C.kc + ok, C.lk[k], dk + k * L::WPS * 1024);
 #pragma unroll
-  for (int k = 0; k < L::NPWV; ++k) lds_copy16(C.vc + ov, C.lv[k], dv + k * 4096);
+  for (int k = 0; k < L::NPWV; ++k) lds_copy16(C.vc + ov, C.lv[k], dv + k * L::WPS * 1024);
   if (C.s_arr_on) {
     const uint64_t os = static_cast<uint64_t>(pg) * C.sp_b + of * C.sp_p;
     if (C.s_on) lds_copy16(C.sp + os, C.ls, buf + C.s_lds);
@@ -1273,7 +1320,11 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
   for (int x = 0; x < 2; ++x) {
     const uint8_t* kp = buf + L::K_OFF + x * 16 * L::CROWK;
     const int kb = wave * L::HBK + blk * KLB;
-    if constexpr (KLB == 32) {
+    if constexpr (KLB == 64) {          // fp16 K: a quarter row, 32 halves
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        st[x].k.v[j] = *reinterpret_cast<const uint4*>(kp + L::code_off(L::CROWK, col, kb + 16 * j));
+    } else if constexpr (KLB == 32) {
       st[x].k.v = *reinterpret_cast<const uint4*>(kp + L::code_off(L::CROWK, col, kb));
       st[x].k.w = *reinterpret_cast<const uint4*>(kp + L::code_off(L::CROWK, col, kb + 16));
     } else if constexpr (KLB == 16) {
@@ -1281,10 +1332,12 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
     } else {
       st[x].k.v = *reinterpret_cast<const uint2*>(kp + L::code_off(L::CROWK, col, kb));
     }
-    halves_from_lds<NGK>(st[x].ks, buf + L::KS_OFF + x * 16 * L::SROWK +
-                                       L::scale_off(L::SROWK, col, wave * L::SBK));
-    halves_from_lds<NG>(st[x].vs, buf + L::VS_OFF + x * 16 * L::SROWV +
-                                      L::scale_off(L::SROWV, col, wave * L::SBV));
+    if constexpr (L::SBK > 0)
+      halves_from_lds<NGK>(st[x].ks, buf + L::KS_OFF + x * 16 * L::SROWK +
+                                         L::scale_off(L::SROWK, col, wave * L::SBK));
+    if constexpr (L::SBV > 0)
+      halves_from_lds<NG>(st[x].vs, buf + L::VS_OFF + x * 16 * L::SROWV +
+                                        L::scale_off(L::SROWV, col, wave * L::SBV));
     if constexpr (KASYM)
       halves_from_lds<NG>(st[x].kz, buf + L::KZ_OFF + x * 16 * L::SROWK +
                                         L::scale_off(L::SROWK, col, wave * L::SBK));
@@ -1298,11 +1351,27 @@ __device__ __forceinline__ void coop_read(const uint8_t* buf, int wave, int col,
 // D/32 bytes at columns (D/16)*col.. of token 16x + 4blk + i.  The four lane
 // blocks read rows 4blk + i, whose chunk swizzles differ, so the 64 lanes
 // hit 64 distinct banks.
-template <class L, int D, bool PAIRS = false, class VW>
+//
+// fp16 V (16 bytes per lane and token: the 8 halves of columns 8 col ..
+// 8 col + 7): rows of a masked tile's tokens past t_end are read as 0, since
+// the bytes there are stale and could hold Inf or NaN, which a zero
+// probability would not cancel.
+template <class L, int D, bool PAIRS = false, bool MASK = false, class VW>
 __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int col, int blk,
-                                            VW (&vw)[2][4]) {
+                                            VW (&vw)[2][4], int tb = 0, int t_end = 0) {
   constexpr int CB = L::HBV / 16;      // V code bytes per lane and token: 8 columns
-  if constexpr (PAIRS) {
+  if constexpr (CB == 16) {
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int o = L::V_OFF + x * 16 * L::CROWV +
+                      L::code_off(L::CROWV, 4 * blk + i, wave * L::HBV + 16 * col);
+        const uint4 v = *reinterpret_cast<const uint4*>(buf + o);
+        const bool ok = !MASK || tb + 16 * x + 4 * blk + i < t_end;
+        vw[x][i] = ok ? v : uint4{0u, 0u, 0u, 0u};
+      }
+  } else if constexpr (PAIRS) {
     // columns 4 col .. 4 col + 3 (groups 0-1) in the low half, 64 + 4 col ..
     // (groups 2-3) in the high half
 #pragma unroll
@@ -1317,21 +1386,23 @@ __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int co
             buf + base + L::code_off(L::CROWV, 4 * blk + i, b0 + D / 4));
         vw[x][i] = lo | (hi << 16);
       }
-    return;
+  } else {
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int o = L::V_OFF + x * 16 * L::CROWV +
+                      L::code_off(L::CROWV, 4 * blk + i, wave * L::HBV + CB * col);
+        if constexpr (CB == 8)
+          vw[x][i] = *reinterpret_cast<const uint2*>(buf + o);
+        else if constexpr (CB == 4)
+          vw[x][i] = *reinterpret_cast<const uint32_t*>(buf + o);
+        else
+          vw[x][i] = *reinterpret_cast<const uint16_t*>(buf + o);
+      }
   }
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int o = L::V_OFF + x * 16 * L::CROWV +
-                    L::code_off(L::CROWV, 4 * blk + i, wave * L::HBV + CB * col);
-      if constexpr (CB == 8)
-        vw[x][i] = *reinterpret_cast<const uint2*>(buf + o);
-      else if constexpr (CB == 4)
-        vw[x][i] = *reinterpret_cast<const uint32_t*>(buf + o);
-      else
-        vw[x][i] = *reinterpret_cast<const uint16_t*>(buf + o);
-    }
+  (void)tb;
+  (void)t_end;
 }
 
 // One tile, software-pipelined with the previous one: start the copy of tile
@@ -1374,7 +1445,7 @@ __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int 
     }
   }
   // tile i's V replaces tile i - 1's in place once its PV has consumed it
-  coop_read_v<L, D, WS::PAIRS_OK && NSET == 1>(cur, wave, col, blk, vw);
+  coop_read_v<L, D, WS::PAIRS_OK && NSET == 1, MASK>(cur, wave, col, blk, vw, tb, t_end);
   _Float16 sv[2][WS::NGV];
   const float svmax = W[0].template vscales<MASK>(st, valid, sv);
 #pragma unroll
@@ -1590,13 +1661,21 @@ struct StreamStart {
 //  V   read from LDS as byte pairs: byte 16 m + col of two tokens in the two
 //      halves of a dword, one mask per nibble (kNib1 / kNib16).
 // ---------------------------------------------------------------------------
-template <int NGV, bool VASYM>
+//
+// K INT4 in two scale groups (D = 128, g64; V then has the same two groups)
+// fits the same lane layout: QK rows (g, K group) are 2 g + kg, as in
+// WaveState with NG = 2, so only the PV differs from WaveState there.
+template <int NGV, bool VASYM, bool K8 = true, bool KASYM = false>
 struct WaveStateW {
   static constexpr int NCH = 4;                 // D = 128
   static constexpr int GPL = 2;                 // heads per lane
-  using ST = SubTile<4, NGV, 8, 1, 4>;          // INT8 K, one scale per row
-  h8 aq[NCH];          // q rows 2g, 2g + 1 = head g (A operands of QK)
-  f4 cinit;            // QK accumulator start: -128 * 2^-24 * sum(q) (biased codes)
+  static constexpr int KCH = K8 ? 8 : 4;        // K code dwords per lane and token
+  static constexpr int NGK = K8 ? 1 : 2;        // K scale groups
+  static_assert(K8 ? !KASYM : NGV == 2, "INT8 K per row, or INT4 K in V's two groups");
+  using ST = SubTile<4, NGV, KCH, NGK, 4>;
+  h8 aq[NCH];          // q rows 2g + part (A operands of QK)
+  f4 cinit;            // QK accumulator start: -bias * 2^-24 * sum(q over the row)
+  float qsum24[4];     // 2^-24 * sum(q) of rows 4 blk + i (asymmetric INT4 K)
   h4 eye;              // identity, B operand of the P' transposes
   f4 acc[4][2];        // [column block m][nibble h]: rows (g, hi/lo)
   float m_run[GPL], lsum[GPL], sl2[GPL], thr[GPL];
@@ -1610,15 +1689,29 @@ struct WaveStateW {
                                          float (&score)[2][GPL]) const {
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-      f4 S = cinit;
+      f4 S = KASYM ? f4{0.f, 0.f, 0.f, 0.f} : cinit;
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
         S = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            aq[c], bytes_to_h8_sub(st[x].k.dw(2 * c), st[x].k.dw(2 * c + 1)), S, 0, 0, 0);
-      const float sk = st[x].ks.get(0);
+            aq[c],
+            K8 ? bytes_to_h8_sub(st[x].k.dw(2 * c), st[x].k.dw(2 * c + 1))
+               : nibbles_to_h8_sub(st[x].k.dw(c)),
+            S, 0, 0, 0);
 #pragma unroll
-      for (int gi = 0; gi < GPL; ++gi)
-        score[x][gi] = (MASK && !valid[x]) ? -INFINITY : sk * S[2 * gi];
+      for (int gi = 0; gi < GPL; ++gi) {
+        float sc;
+        if constexpr (K8) {
+          sc = st[x].ks.get(0) * S[2 * gi];            // rows 2 gi, 2 gi + 1 are equal
+        } else {
+          sc = 0.0f;
+#pragma unroll
+          for (int kg = 0; kg < 2; ++kg) {
+            if constexpr (KASYM) sc = fmaf(st[x].kz.get(kg), qsum24[2 * gi + kg], sc);
+            sc = fmaf(st[x].ks.get(kg), S[2 * gi + kg], sc);
+          }
+        }
+        score[x][gi] = (MASK && !valid[x]) ? -INFINITY : sc;
+      }
     }
   }
 
@@ -1742,13 +1835,17 @@ struct WaveStateW {
 
 // q rows (two per head), constants and accumulators of the wave serving kv
 // head `kvh` with all its G <= 8 query heads (qw from load_q<128, 2>: lane
-// (col, blk) holds elements 32 blk .. 32 blk + 31 of head col / 2).
-template <int NGV, bool VASYM>
-__device__ __forceinline__ void init_wave_w(WaveStateW<NGV, VASYM>& W, const uint4 (&qw)[4],
-                                            const DecodeArgs& a, int col, int blk) {
+// (col, blk) holds elements 32 blk .. 32 blk + 31 of head col / 2).  INT8 K:
+// both rows of a head carry all of q; INT4 K: row 2 g + kg carries the
+// elements of K group kg (the lane's elements, 32 blk .. 32 blk + 31, lie in
+// group blk / 2), in the nibble slot order with q / 16 facing odd nibbles.
+template <int NGV, bool VASYM, bool K8, bool KASYM>
+__device__ __forceinline__ void init_wave_w(WaveStateW<NGV, VASYM, K8, KASYM>& W,
+                                            const uint4 (&qw)[4], const DecodeArgs& a, int col,
+                                            int blk) {
   const bool qneg = a.scale_log2 < 0.0f;
   const bool qzero = a.scale_log2 == 0.0f;
-  const bool on = col < 2 * a.group && !qzero;
+  const bool on = col < 2 * a.group && !qzero && (K8 || blk / 2 == col % 2);
   uint16_t qv[32];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -1775,18 +1872,21 @@ __device__ __forceinline__ void init_wave_w(WaveStateW<NGV, VASYM>& W, const uin
   for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int el = 8 * c + kByteK8[e];
+      const int el = 8 * c + (K8 ? kByteK8[e] : kNibK[e]);
       _Float16 v = !on ? _Float16(0)
                    : a.q_bf16 ? static_cast<_Float16>(bf16_bits_to_float(qv[el]) * qscale)
                               : __builtin_bit_cast(_Float16, qv[el]);
       if (qneg) v = -v;
-      W.aq[c][e] = v;
+      W.aq[c][e] = (!K8 && (e & 2)) ? v * static_cast<_Float16>(0.0625f) : v;
       qpart += static_cast<float>(v);
     }
   qpart += __shfl_xor(qpart, 16, kWave);
   qpart += __shfl_xor(qpart, 32, kWave);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) W.cinit[i] = -128.0f * (__shfl(qpart, 4 * blk + i, kWave) * 0x1p-24f);
+  for (int i = 0; i < 4; ++i) {
+    W.qsum24[i] = __shfl(qpart, 4 * blk + i, kWave) * 0x1p-24f;
+    W.cinit[i] = KASYM ? 0.0f : (K8 ? -128.0f : -8.0f) * W.qsum24[i];
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) W.eye[e] = (blk == col / 4 && e == col % 4) ? 1.0f : 0.0f;
 #pragma unroll
@@ -1807,9 +1907,10 @@ __device__ __forceinline__ void init_wave_w(WaveStateW<NGV, VASYM>& W, const uin
 
 // The wave's partial (acc, max, sum) for each of its kv head's G query heads
 // at entry base + g * stride.
-template <int NGV, bool VASYM>
-__device__ __forceinline__ void write_partials_w(WaveStateW<NGV, VASYM>& W, const DecodeArgs& a,
-                                                 int64_t base, int64_t stride, int col, int blk) {
+template <int NGV, bool VASYM, bool K8, bool KASYM>
+__device__ __forceinline__ void write_partials_w(WaveStateW<NGV, VASYM, K8, KASYM>& W,
+                                                 const DecodeArgs& a, int64_t base, int64_t stride,
+                                                 int col, int blk) {
   const int G = a.group;
   const float kinv = ldexpf(1.0f, -static_cast<int>(W.kexp));
 #pragma unroll
@@ -1831,7 +1932,7 @@ __device__ __forceinline__ void write_partials_w(WaveStateW<NGV, VASYM>& W, cons
           const float hl = gi ? v[2] + v[3] : v[0] + v[1];
           // high nibbles arrive as 16 n: a factor 16 fewer
           a.part_o[row * 128 + 32 * m + 2 * col + h] =
-              fmaf(hl, h ? 0x1p20f : 0x1p24f, W.zacc[gi][WaveStateW<NGV, VASYM>::vg_of(m)]) * kinv;
+              fmaf(hl, h ? 0x1p20f : 0x1p24f, W.zacc[gi][W.vg_of(m)]) * kinv;
         }
       if (col == 0) {
         a.part_ml[2 * row] = W.m_run[gi] * W.sl2[gi];
@@ -1863,18 +1964,19 @@ __device__ __forceinline__ void coop_read_v_w(const uint8_t* buf, int wave, int 
 // One tile of the wide-group kernel, pipelined as coop_tile: copies of tile
 // i + NBUF - 1, this wave's slice of tile i, QK of tile i next to PV of tile
 // i - 1, tile i's V into the registers PV has consumed, then P' of tile i.
-template <class L, int NGV, bool VASYM, bool MASK, bool PV_PREV>
-__device__ __forceinline__ void coop_tile_w(WaveStateW<NGV, VASYM>& W, const CoopAddr& C, int i,
+template <class L, int NGV, bool VASYM, bool K8, bool KASYM, bool MASK, bool PV_PREV>
+__device__ __forceinline__ void coop_tile_w(WaveStateW<NGV, VASYM, K8, KASYM>& W, const CoopAddr& C,
+                                            int i,
                                             int ntiles, int t_begin, int t_end, int wave, int col,
                                             int blk, const uint8_t* cur, uint8_t* nxt,
                                             uint32_t (&vb)[4][4], h8 (&aw)[NGV], PageWindow& PW,
                                             int lane) {
-  using WS = WaveStateW<NGV, VASYM>;
+  using WS = WaveStateW<NGV, VASYM, K8, KASYM>;
   constexpr int NBUF = L::NBUF;
   const int tb = t_begin + 32 * i;
   if (i + NBUF - 1 < ntiles) coop_issue<L>(C, PW, lane, wave, tb + 32 * (NBUF - 1), t_end, nxt);
   typename WS::ST st[2];
-  coop_read<L, false, VASYM>(cur, wave, col, blk, st);
+  coop_read<L, KASYM, VASYM>(cur, wave, col, blk, st);
   bool valid[2] = {true, true};
   if constexpr (MASK) {
     valid[0] = tb + col < t_end;
@@ -1899,19 +2001,23 @@ __device__ __forceinline__ void coop_tile_w(WaveStateW<NGV, VASYM>& W, const Coo
 // s * heads_per_set.  Returns without work (uniformly) when the segment is
 // empty.
 // WIDE: the wide-group wave state (WaveStateW: one set for 5 <= G <= 8,
-// INT8 K with one scale per row, INT4 V with NG groups, D = 128).
+// INT8 K with one scale per row, INT4 V with NG groups, D = 128).  K16 / V16:
+// fp16 K (4 kv heads per block) / fp16 V.
 template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8,
-          bool WIDE = false>
-__device__ __forceinline__ void coop_segment(const DecodeArgs& a,
-                                             uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8>::NBUF]
-                                                           [CoopLayout<D, NG, K8, NGK, V8>::BYTES],
-                                             int seq, int hg, int t_begin, int seg_tokens,
-                                             int seq_len_known, int64_t base0, int64_t stride) {
-  using L = CoopLayout<D, NG, K8, NGK, V8>;
+          bool WIDE = false, bool K16 = false, bool V16 = false>
+__device__ __forceinline__ void coop_segment(
+    const DecodeArgs& a,
+    uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8, K16, V16>::NBUF]
+                  [CoopLayout<D, NG, K8, NGK, V8, K16, V16>::BYTES],
+    int seq, int hg, int t_begin, int seg_tokens, int seq_len_known, int64_t base0,
+    int64_t stride) {
+  using L = CoopLayout<D, NG, K8, NGK, V8, K16, V16>;
   constexpr int NCH = D / 32;
-  constexpr int KCH = K8 ? 2 * NCH : NCH;
+  constexpr int KCH = K16 ? 4 * NCH : K8 ? 2 * NCH : NCH;
   constexpr int NBUF = L::NBUF;
-  using WS = WaveState<NCH, NG, KASYM, VASYM, KCH, NGK, V8>;
+  constexpr int KEB = K16 ? 2 : 1;    // bytes per element of the K / V arrays
+  constexpr int VEB = V16 ? 2 : 1;    // (their strides are in elements)
+  using WS = WaveState<NCH, NG, KASYM, VASYM, KCH, NGK, V8, V16>;
   // An opaque thread index: the stream schedule runs this once per segment
   // in a loop, and lane-derived set-up hoisted out of that loop would stay
   // live in VGPRs through every segment's tile loop (+50 VGPRs, and spills
@@ -1928,31 +2034,32 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
   {
     const knlp_kv_plane& K = a.kp;
     const knlp_kv_plane& V = a.vp;
-    C.kc = static_cast<const uint8_t*>(K.data) + h0 * K.stride_head;
-    C.vc = static_cast<const uint8_t*>(V.data) + h0 * V.stride_head;
-    C.kc_b = static_cast<uint32_t>(K.stride_block);
-    C.kc_p = static_cast<uint32_t>(K.stride_page);
-    C.vc_b = static_cast<uint32_t>(V.stride_block);
-    C.vc_p = static_cast<uint32_t>(V.stride_page);
-    C.same_kv = K.stride_block == V.stride_block && K.stride_page == V.stride_page;
+    C.kc = static_cast<const uint8_t*>(K.data) + KEB * h0 * K.stride_head;
+    C.vc = static_cast<const uint8_t*>(V.data) + VEB * h0 * V.stride_head;
+    C.kc_b = static_cast<uint32_t>(KEB * K.stride_block);
+    C.kc_p = static_cast<uint32_t>(KEB * K.stride_page);
+    C.vc_b = static_cast<uint32_t>(VEB * V.stride_block);
+    C.vc_p = static_cast<uint32_t>(VEB * V.stride_page);
+    C.same_kv = C.kc_b == C.vc_b && C.kc_p == C.vc_p;
     // code copy: lane -> LDS byte part*1024 + 16*lane of a sub-tile, which
-    // holds logical chunk (physical chunk) ^ row of that row
+    // holds logical chunk (physical chunk) ^ row of that row; this wave's
+    // parts are (wave >> 1) + WPS k
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int byte = ((wave >> 1) + 4 * k) % L::CPSK * 1024 + 16 * lane;
+    for (int k = 0; k < L::NPWK; ++k) {
+      const int byte = ((wave >> 1) + L::WPS * k) % L::CPSK * 1024 + 16 * lane;
       const int r = byte / L::CROWK;
       const int c = ((byte % L::CROWK) >> 4) ^ r;
-      C.lk[k] = static_cast<uint32_t>(r * K.stride_page + 16 * c);
+      C.lk[k] = static_cast<uint32_t>(r * C.kc_p + 16 * c);
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int byte = ((wave >> 1) + 4 * k) % L::CPSV * 1024 + 16 * lane;
+    for (int k = 0; k < L::NPWV; ++k) {
+      const int byte = ((wave >> 1) + L::WPS * k) % L::CPSV * 1024 + 16 * lane;
       const int r = byte / L::CROWV;
       const int c = ((byte % L::CROWV) >> 4) ^ r;
-      C.lv[k] = static_cast<uint32_t>(r * V.stride_page + 16 * c);
+      C.lv[k] = static_cast<uint32_t>(r * C.vc_p + 16 * c);
     }
-    // wave w copies scale array w / 2 (ks, vs, kz, vz) of sub-tile w % 2
-    const int arr = wave >> 1;
+    // wave w copies scale array L::s_array(w) (ks, vs, kz, vz) of sub-tile w % 2
+    const int arr = L::s_array(wave);
     C.x = wave & 1;
     const uint16_t* base = arr == 0 ? static_cast<const uint16_t*>(K.scales)
                          : arr == 1 ? static_cast<const uint16_t*>(V.scales)
@@ -1964,14 +2071,17 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
                       : arr == 2 ? K.z_stride_block : V.z_stride_block;
     const int64_t spg = arr == 0 ? K.s_stride_page : arr == 1 ? V.s_stride_page
                       : arr == 2 ? K.z_stride_page : V.z_stride_page;
-    const bool arr_on = arr < 2 || (arr == 2 && KASYM) || (arr == 3 && VASYM);
+    // (fp16 planes have no scales or zero-points)
+    const bool arr_on = (arr == 0 && !K16) || (arr == 1 && !V16) || (arr == 2 && KASYM) ||
+                        (arr == 3 && VASYM);
     const int srow = L::s_row(arr);
     C.s_arr_on = arr_on;
     C.s_on = arr_on && lane < srow;
     C.sp = arr_on ? reinterpret_cast<const uint8_t*>(base + h0 * sh) : nullptr;
     C.sp_b = static_cast<uint32_t>(2 * sbk);
     C.sp_p = static_cast<uint32_t>(2 * spg);
-    {
+    C.ls = 0;
+    if (arr_on) {
       const int byte = 16 * lane;
       const int r = byte / srow;
       const int c = ((byte % srow) >> 4) ^ L::scale_swz(srow, r);
@@ -1989,7 +2099,8 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
   // wait for these loads (whose counter the copies share) holds up the
   // copies in flight.
   const int seq_len_raw = seq_len_known >= 0 ? seq_len_known : a.seq_lens[seq];
-  static_assert(!WIDE || (D == 128 && K8 && NGK == 1 && !V8 && !KASYM && NSET == 1),
+  static_assert(!WIDE || (D == 128 && !V8 && NSET == 1 &&
+                          (K8 ? NGK == 1 && !KASYM : NGK == 2 && NG == 2)),
                 "the wide-group wave state's shapes");
   uint4 qw[NSET][D / 32];
   if constexpr (WIDE) {
@@ -2018,14 +2129,15 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
     if (t < ntiles) coop_issue<L>(C, PW, lane, wave, t_begin + 32 * t, t_end, lds[t]);
   const int nfull = (t_end - t_begin) / 32;
   if constexpr (WIDE) {
-    WaveStateW<NG, VASYM> W;
+    WaveStateW<NG, VASYM, K8, KASYM> W;
     init_wave_w(W, qw[0], a, col, blk);
     wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
     __syncthreads();
     uint32_t vb[4][4];
     h8 aw[NG];
 #define KNLP_COOP_TILE_W(MASK, PV_PREV)                                                     \
-  coop_tile_w<L, NG, VASYM, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end, wave, col, blk, \
+  coop_tile_w<L, NG, VASYM, K8, KASYM, MASK, PV_PREV>(W, C, i, ntiles, t_begin, t_end,      \
+                                                      wave, col, blk,                      \
                                            lds[i % NBUF], lds[(i + NBUF - 1) % NBUF], vb,   \
                                            aw, PW, lane)
     int i = 0;
@@ -2045,8 +2157,8 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
   WS W[NSET];
 #pragma unroll
   for (int s = 0; s < NSET; ++s)
-    init_wave<D, NG, KASYM, VASYM, KCH, NGK, V8>(W[s], qw[s], a, col, blk,
-                                                 s * heads_per_set<NG>());
+    init_wave<D, NG, KASYM, VASYM, KCH, NGK, V8, V16>(W[s], qw[s], a, col, blk,
+                                                      s * heads_per_set<NG>());
   wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
@@ -2073,7 +2185,7 @@ __device__ __forceinline__ void coop_segment(const DecodeArgs& a,
       W[s].template pv_columns<true>(vw, ahi[s], alo[s]);
     else
       W[s].pv_columns(vw, ahi[s], alo[s]);
-    write_partials_at<D, NG, KASYM, VASYM, true, KCH, NGK, V8, false, PAIRS>(
+    write_partials_at<D, NG, KASYM, VASYM, true, KCH, NGK, V8, V16, PAIRS>(
         W[s], a, base0 + s * heads_per_set<NG>() * stride, stride, col, blk,
         s * heads_per_set<NG>());
   }
@@ -2130,11 +2242,12 @@ struct StreamWalk {
 // allocation: the stream loop's state would otherwise cost the split kernel
 // registers through its whole tile loop).
 template <bool STREAM, int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8,
-          bool WIDE>
+          bool WIDE, bool K16 = false, bool V16 = false>
 __device__ __forceinline__ void coop_kernel_body(
     const DecodeArgs& a,
-    uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8>::NBUF][CoopLayout<D, NG, K8, NGK, V8>::BYTES]) {
-  using L = CoopLayout<D, NG, K8, NGK, V8>;
+    uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8, K16, V16>::NBUF]
+                  [CoopLayout<D, NG, K8, NGK, V8, K16, V16>::BYTES]) {
+  using L = CoopLayout<D, NG, K8, NGK, V8, K16, V16>;
   static_assert(!(K8 && KASYM) && !(V8 && VASYM), "INT8 codes are symmetric");
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   if constexpr (!STREAM) {
@@ -2142,7 +2255,7 @@ __device__ __forceinline__ void coop_kernel_body(
     const int seq = blockIdx.y;
     const int hg = blockIdx.z;
     const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + (hg * L::kHeads + wave) * a.group;
-    coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE>(
+    coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16>(
         a, lds, seq, hg, split * a.split_tokens, a.split_tokens, -1,
         row0 * a.num_splits + split, a.num_splits);
   } else {
@@ -2210,7 +2323,7 @@ __device__ __forceinline__ void coop_kernel_body(
       KArgs* kp = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
       asm volatile("" : "+s"(kp));
       const DecodeArgs& A = *(const DecodeArgs*)kp;
-      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE>(
+      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16>(
           A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
           static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
       StreamWalk V = StreamWalk::uniform(walk);
@@ -2249,6 +2362,25 @@ void decode_mfma_coop_stream_kernel(DecodeArgs a) {
   using L = CoopLayout<D, NG, K8, NGK, V8>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[L::NBUF][L::BYTES];
   coop_kernel_body<true, D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE>(a, lds);
+}
+
+// fp16 K (and fp16, INT4 or INT8 V) on the cooperative loader: 4 kv heads
+// per block (one wave each), one block per CU, so a wave may use the whole
+// register file of its SIMD lane.
+template <int D, int NG, bool VASYM, bool V8, bool V16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+void decode_mfma_coop16_kernel(DecodeArgs a) {
+  using L = CoopLayout<D, NG, false, NG, V8, true, V16>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::NBUF][L::BYTES];
+  coop_kernel_body<false, D, NG, false, VASYM, false, NG, 1, V8, false, true, V16>(a, lds);
+}
+
+template <int D, int NG, bool VASYM, bool V8, bool V16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+void decode_mfma_coop16_stream_kernel(DecodeArgs a) {
+  using L = CoopLayout<D, NG, false, NG, V8, true, V16>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::NBUF][L::BYTES];
+  coop_kernel_body<true, D, NG, false, VASYM, false, NG, 1, V8, false, true, V16>(a, lds);
 }
 
 inline int heads_per_block_mfma(int num_kv_heads) {

@@ -10,8 +10,44 @@
 namespace knlp {
 namespace {
 
+// fp16 K on the cooperative loader (4 kv heads per block): fp16 V, or INT4 /
+// INT8 V in 2 or 4 scale groups with one head set, D = 128 (with one V scale
+// per row the block's heads' scales of a token are 8 bytes, less than the
+// 16-byte chunk a lane copies: the per-head kernel takes that shape).
+template <bool STREAM>
+int launch_coop16(const DecodeArgs& a, int head_size, hipStream_t stream) {
+  if (head_size != 128) return KNLP_ERR_SHAPE;
+  const int ng = a.vp.format == KNLP_KV_FP16 ? 1 : head_size / a.vp.group_size;
+  const bool va = a.vp.format == KNLP_KV_INT4_ASYM;
+  const bool v8 = a.vp.format == KNLP_KV_INT8_SYM;
+  const bool v16 = a.vp.format == KNLP_KV_FP16;
+  if (a.group * ng > 16) return KNLP_ERR_SHAPE;
+  const dim3 grid = STREAM ? dim3(a.stream) : dim3(a.num_splits, a.num_seqs, a.num_kv_heads / 4);
+  const dim3 block(kWave * 4);
+#define KNLP_LAUNCH_COOP16(...)                                                            \
+  do {                                                                                     \
+    if constexpr (STREAM)                                                                  \
+      hipLaunchKernelGGL((decode_mfma_coop16_stream_kernel<__VA_ARGS__>), grid, block, 0,  \
+                         stream, a);                                                       \
+    else                                                                                   \
+      hipLaunchKernelGGL((decode_mfma_coop16_kernel<__VA_ARGS__>), grid, block, 0, stream, \
+                         a);                                                               \
+  } while (0)
+  if (v16) KNLP_LAUNCH_COOP16(128, 1, false, false, true);
+  else if (v8 && ng == 4) KNLP_LAUNCH_COOP16(128, 4, false, true, false);
+  else if (v8) return KNLP_ERR_SHAPE;
+  else if (ng == 4) { if (va) KNLP_LAUNCH_COOP16(128, 4, true, false, false);
+                      else KNLP_LAUNCH_COOP16(128, 4, false, false, false); }
+  else if (ng == 2) { if (va) KNLP_LAUNCH_COOP16(128, 2, true, false, false);
+                      else KNLP_LAUNCH_COOP16(128, 2, false, false, false); }
+  else return KNLP_ERR_SHAPE;
+#undef KNLP_LAUNCH_COOP16
+  return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
+}
+
 template <bool STREAM>
 int launch_coop(const DecodeArgs& a, int head_size, hipStream_t stream) {
+  if (a.kp.format == KNLP_KV_FP16) return launch_coop16<STREAM>(a, head_size, stream);
   const int ng = head_size / a.vp.group_size;
   const bool k8 = a.kp.format == KNLP_KV_INT8_SYM;
   const int ngk = head_size / a.kp.group_size;
@@ -52,11 +88,20 @@ int launch_coop(const DecodeArgs& a, int head_size, hipStream_t stream) {
     if (va) KNLP_LAUNCH_COOP(128, NG, false, true, true, NGK, 2);                         \
     else KNLP_LAUNCH_COOP(128, NG, false, false, true, NGK, 2);                           \
   }
-  // INT8 K with one scale per row, INT4 V in four groups, 5 <= G <= 8: the
-  // wide-group wave state (one head set; kv_decode_mfma.h, WaveStateW)
+  // The wide-group wave state (kv_decode_mfma.h, WaveStateW: two QK rows
+  // per head, PV per V group): INT8 K with one scale per row and INT4 V in
+  // four groups at 5 <= G <= 8 (one head set instead of two), and INT4 K
+  // and V in two groups at G <= 8 (PV products within one group)
   if (k8 && !v8 && head_size == 128 && ng == 4 && ngk == 1 && a.group >= 5 && a.group <= 8) {
     if (va) KNLP_LAUNCH_COOP(128, 4, false, true, true, 1, 1, false, true);
     else KNLP_LAUNCH_COOP(128, 4, false, false, true, 1, 1, false, true);
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
+  }
+  if (!k8 && !v8 && head_size == 128 && ng == 2 && a.group <= 8) {
+    if (ka && va) KNLP_LAUNCH_COOP(128, 2, true, true, false, 2, 1, false, true);
+    else if (ka) KNLP_LAUNCH_COOP(128, 2, true, false, false, 2, 1, false, true);
+    else if (va) KNLP_LAUNCH_COOP(128, 2, false, true, false, 2, 1, false, true);
+    else KNLP_LAUNCH_COOP(128, 2, false, false, false, 2, 1, false, true);
     return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
   }
 #define KNLP_INT8K(NG)                                                                    \

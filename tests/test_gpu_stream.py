@@ -55,6 +55,14 @@ CASES = [
      1, 32, 32),
     ("charged_two_rows_per_seq", _lens(24, 1, 3000, 4), 64, 16, 128, 1, 1, 32, 32),
     ("charged_kint8_row_two_sets", _lens(30, 1, 3000, 6, zeros=2), 40, 8, 128, 2, 1, 128, 32),
+    # fp16 K on the cooperative loader (4 kv heads per block): fp16, INT4 and
+    # INT8 V; ragged rows, empty sequences, charges
+    ("fp16_fp16", [1, 17, 33, 0, 900, 2049], 32, 8, 128, 3, 3, 128, 128),
+    ("fp16_fp16_hkv4_g5", [700, 31, 64], 20, 4, 128, 3, 3, 128, 128),
+    ("kfp16_vint4_asym", [600, 5, 0, 1500], 32, 8, 128, 3, 1, 128, 32),
+    ("kfp16_vint4_sym_g64", [800, 65], 32, 8, 128, 3, 0, 128, 64),
+    ("kfp16_vint8_g32", [500, 48, 1], 16, 4, 128, 3, 2, 128, 32),
+    ("charged_fp16_fp16", _lens(40, 1, 3000, 7, zeros=2), 32, 8, 128, 3, 3, 128, 128),
 ]
 
 
@@ -87,8 +95,9 @@ def test_stream_schedule_bf16_query():
 
 @pytest.mark.parametrize("case", [
     # name, seq_lens, hq, hkv, d, kfmt, vfmt, kgs, vgs: planes the cooperative
-    # kernel does not take run split-K inside the stream workspace
-    ("fp16_k_vint4", [700, 1, 0, 65], 32, 8, 128, 3, 1, 128, 32),
+    # kernel does not take run split-K inside the stream workspace (fp16 K at
+    # D = 64, Hkv % 8 != 0 with packed K)
+    ("fp16_k_d64_vint4", [700, 1, 0, 65], 32, 8, 64, 3, 1, 64, 32),
     ("hkv4_int4", [900, 33], 16, 4, 128, 1, 1, 32, 32),
     ("hkv4_kint8_valu", [300, 48, 0], 16, 4, 128, 2, 1, 128, 32),
 ], ids=lambda c: c[0])
