@@ -8,15 +8,24 @@
 // reference's acc / l_i with l_i = 0 (F:886-887).
 //
 // Few partials per (sequence, q head) in a large batch: one wave per head
-// folds them (merge_wave_kernel).  Otherwise one block of NW waves per
-// (sequence, q head), wave w folds splits w, w+NW, ... with an online (max-rescaling)
-// combine, then the NW wave states are combined through LDS.  NW grows with
-// the split count (4, 8 or 16 waves) so that a wave folds at most a few
-// groups of U splits: config 4 (one sequence, 256 splits) merges in about a
-// third of the time 4 waves take.
+// folds them (merge_wave_kernel).  Few heads with many partials each (one
+// or a few sequences at long context): one workgroup per 16-dim slice of a
+// head (merge_slice_kernel), so that the batch still spreads over the CUs.
+// Otherwise one block of NW waves per (sequence, q head), wave w folds
+// splits w, w+NW, ... with an online (max-rescaling) combine, then the NW
+// wave states are combined through LDS.  NW grows with the split count (4, 8
+// or 16 waves) so that a wave folds at most a few groups of U splits.
 #include "kv_decode.h"
 
 namespace knlp {
+
+// merge_slice_kernel takes batches of at most kSliceMaxRows (sequence, q
+// head) rows with at least kSliceMinSplits partials per row.  At B = 1,
+// T = 32768 (32 heads of 128 partials) it shortens the decode step from
+// 20.4 to 18.3 us; at config 2's 256 heads of 32 partials a threshold of 16
+// made the step 1.3 us longer than merge_kernel, hence 64.
+constexpr int kSliceMinSplits = 64;
+constexpr int64_t kSliceMaxRows = 256;
 
 // The partials of (seq, h): entries row0 + i * stride, i < ns.
 struct MergeRows {
@@ -207,6 +216,107 @@ __global__ __launch_bounds__(HPW * 64) void merge_wave_kernel(
     store_out(out, out_bf16, seq * o_stride_seq + h * o_stride_head + lane * E + e, o[e] / L);
 }
 
+// Fold partials i = first, first + step, ... < ns of one (sequence, q head)
+// for one dimension d: N loads in flight per group, then the remainder in
+// groups of 4, 2 and 1 (every load of a real partial, as in fold_partials).
+template <int D, int N>
+__device__ __forceinline__ void fold_dim_group(const float* __restrict__ part_o,
+                                               const float* __restrict__ part_ml,
+                                               const MergeRows& R, int first, int step, int d,
+                                               float& M, float& L, float& o) {
+  float mi[N], li[N], oi[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int64_t ent = R.row0 + static_cast<int64_t>(first + step * u) * R.stride;
+    mi[u] = part_ml[2 * ent];
+    li[u] = part_ml[2 * ent + 1];
+    oi[u] = part_o[ent * D + d];
+  }
+  float mn = M;
+#pragma unroll
+  for (int u = 0; u < N; ++u) mn = fmaxf(mn, mi[u]);
+  if (mn == -INFINITY) return;
+  const float a_old = exp2f(M - mn);
+  L *= a_old;
+  o *= a_old;
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const float a = exp2f(mi[u] - mn);
+    L = fmaf(li[u], a, L);
+    o = fmaf(oi[u], a, o);
+  }
+  M = mn;
+}
+
+template <int D, int U>
+__device__ __forceinline__ void fold_dim(const float* __restrict__ part_o,
+                                         const float* __restrict__ part_ml, const MergeRows& R,
+                                         int first, int step, int d, float& M, float& L,
+                                         float& o) {
+  int i = first;
+  for (; i + (U - 1) * step < R.ns; i += U * step)
+    fold_dim_group<D, U>(part_o, part_ml, R, i, step, d, M, L, o);
+  if (i + 3 * step < R.ns) {
+    fold_dim_group<D, 4>(part_o, part_ml, R, i, step, d, M, L, o);
+    i += 4 * step;
+  }
+  if (i + step < R.ns) {
+    fold_dim_group<D, 2>(part_o, part_ml, R, i, step, d, M, L, o);
+    i += 2 * step;
+  }
+  if (i < R.ns) fold_dim_group<D, 1>(part_o, part_ml, R, i, step, d, M, L, o);
+}
+
+// Few (sequence, q head) rows with many partials each (one sequence at long
+// context: 32 rows of 256 partials at config 4).  merge_kernel gives such a
+// batch one workgroup per row, 32 in all, and each pulls its row's 133 KB
+// through one CU (6.6 us for 4.3 MB).  Here a workgroup takes one 16-dim
+// slice of one row, D / 16 workgroups per row: thread t folds dim
+// d0 + t % 16 of partials t / 16, t / 16 + 16, ..., and the 16 split lanes
+// are combined through LDS.  The 16 threads of a split lane fold the same
+// (m, l) pairs (16 lanes loading one address make one request).
+template <int D>
+__global__ __launch_bounds__(256) void merge_slice_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    const int32_t* __restrict__ seq_lens, int hq, int max_context, int split_tokens,
+    int num_splits, void* __restrict__ out, int out_bf16, int64_t o_stride_seq,
+    int64_t o_stride_head, const int32_t* __restrict__ stream_meta,
+    const int32_t* __restrict__ stream_hdr) {
+  constexpr int SD = 16;           // dims per workgroup
+  constexpr int NSL = 256 / SD;    // split lanes
+  static_assert(D % SD == 0, "whole slices");
+  __shared__ float s_o[NSL][SD];
+  __shared__ float s_m[NSL], s_l[NSL];
+  const int h = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int dl = threadIdx.x % SD;
+  const int sl = threadIdx.x / SD;
+  const int d = blockIdx.z * SD + dl;
+  const MergeRows R = merge_rows(seq_lens, seq, h, hq, max_context, split_tokens, num_splits,
+                                 stream_meta, stream_hdr);
+  float M = -INFINITY, L = 0.0f, o = 0.0f;
+  fold_dim<D, 8>(part_o, part_ml, R, sl, NSL, d, M, L, o);
+  if (dl == 0) {
+    s_m[sl] = M;
+    s_l[sl] = L;
+  }
+  s_o[sl][dl] = o;
+  __syncthreads();
+  if (sl != 0) return;
+  float Mg = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NSL; ++k) Mg = fmaxf(Mg, s_m[k]);
+  float Lg = 0.0f, acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NSL; ++k) {
+    // a split lane that saw no partial has M = -inf and contributes nothing
+    const float f = s_m[k] == -INFINITY ? 0.0f : exp2f(s_m[k] - Mg);
+    Lg += s_l[k] * f;
+    acc += s_o[k][dl] * f;
+  }
+  store_out(out, out_bf16, seq * o_stride_seq + h * o_stride_head + d, acc / Lg);
+}
+
 __global__ void stream_header_kernel(int32_t* hdr, int h0, int h1, int h2) {
   if (threadIdx.x == 0) {
     hdr[0] = h0;
@@ -251,6 +361,26 @@ int launch_merge(const float* part_o, const float* part_ml, const int32_t* seq_l
       KNLP_MERGE_WD(256)
 #undef KNLP_MERGE_WD
 #undef KNLP_MERGE_W
+      default:
+        return KNLP_ERR_SHAPE;
+    }
+    return hipGetLastError() == hipSuccess ? KNLP_OK : KNLP_ERR_LAUNCH;
+  }
+  // few rows of many partials: one workgroup per 16-dim slice of a row
+  if (num_splits >= kSliceMinSplits && static_cast<int64_t>(num_seqs) * hq <= kSliceMaxRows) {
+    const dim3 sgrid(hq, num_seqs, head_size / 16);
+    switch (head_size) {
+#define KNLP_MERGE_S(D)                                                                   \
+  case D:                                                                                 \
+    hipLaunchKernelGGL((merge_slice_kernel<D>), sgrid, dim3(256), 0, stream, part_o,      \
+                       part_ml, seq_lens, hq, max_context, split_tokens, num_splits, out, \
+                       out_bf16, o_stride_seq, o_stride_head, stream_meta, stream_hdr);   \
+    break;
+      KNLP_MERGE_S(32)
+      KNLP_MERGE_S(64)
+      KNLP_MERGE_S(128)
+      KNLP_MERGE_S(256)
+#undef KNLP_MERGE_S
       default:
         return KNLP_ERR_SHAPE;
     }
