@@ -664,7 +664,9 @@ struct WaveState {
   // v_perm, then each column's nibble pair is one mask (after one shift per
   // pair of columns): the fp16 subnormal bit patterns of slots (2q, 2q + 1),
   // n * 2^-24 for even j and 16 n * 2^-24 for odd j (h == 1), so the
-  // accumulators acc[c][1] carry an extra factor 16.
+  // accumulators acc[c][1] carry an extra factor 16.  PAIRS (group-pair
+  // layout): vw comes from coop_read_v<PAIRS> already interleaved by token
+  // pairs, and accumulator j holds column 64 (j / 4) + 4 col + j % 4.
   template <bool PAIRS = false>
   __device__ __forceinline__ void pv_columns(const uint32_t (&vw)[2][4], const h8& ahi,
                                              const h8& alo) {
@@ -673,8 +675,13 @@ struct WaveState {
     for (int q = 0; q < 4; ++q) {
       const uint32_t a = vw[q / 2][2 * (q % 2)];
       const uint32_t b = vw[q / 2][2 * (q % 2) + 1];
-      u0[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);   // a.lo16 | b.lo16 << 16
-      u1[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);   // a.hi16 | b.hi16 << 16
+      if constexpr (PAIRS) {      // already token pairs (coop_read_v<PAIRS>)
+        u0[q] = a;
+        u1[q] = b;
+      } else {
+        u0[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);   // a.lo16 | b.lo16 << 16
+        u1[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);   // a.hi16 | b.hi16 << 16
+      }
     }
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -1372,19 +1379,26 @@ __device__ __forceinline__ void coop_read_v(const uint8_t* buf, int wave, int co
         vw[x][i] = ok ? v : uint4{0u, 0u, 0u, 0u};
       }
   } else if constexpr (PAIRS) {
-    // columns 4 col .. 4 col + 3 (groups 0-1) in the low half, 64 + 4 col ..
-    // (groups 2-3) in the high half
+    // token pairs (4 blk + 2p, 4 blk + 2p + 1): vw[x][2p] holds columns
+    // 4 col .. 4 col + 3 (groups 0-1) of the two tokens, one per half,
+    // vw[x][2p + 1] columns 64 + 4 col .. (groups 2-3): one v_perm per word
+    // joins the two 16-bit reads (pv_columns<true> takes them as they are)
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int p = 0; p < 2; ++p) {
         const int base = L::V_OFF + x * 16 * L::CROWV;
         const int b0 = wave * L::HBV + 2 * col;
-        const uint32_t lo = *reinterpret_cast<const uint16_t*>(
-            buf + base + L::code_off(L::CROWV, 4 * blk + i, b0));
-        const uint32_t hi = *reinterpret_cast<const uint16_t*>(
-            buf + base + L::code_off(L::CROWV, 4 * blk + i, b0 + D / 4));
-        vw[x][i] = lo | (hi << 16);
+        const int r = 4 * blk + 2 * p;
+        const auto ld = [&](int row, int byte) {
+          return *reinterpret_cast<const uint16_t*>(buf + base + L::code_off(L::CROWV, row, byte));
+        };
+        // (a two-element vector rather than shifts and ors, so that the
+        // compiler joins the halves with one v_perm and no masking)
+        const u16x2 lo = {ld(r, b0), ld(r + 1, b0)};
+        const u16x2 hi = {ld(r, b0 + D / 4), ld(r + 1, b0 + D / 4)};
+        vw[x][2 * p] = __builtin_bit_cast(uint32_t, lo);
+        vw[x][2 * p + 1] = __builtin_bit_cast(uint32_t, hi);
       }
   } else {
 #pragma unroll
