@@ -1139,13 +1139,23 @@ __global__ __launch_bounds__(V16 ? 256 : 512) void decode_mfma_kernel(DecodeArgs
 // conversions.
 // ---------------------------------------------------------------------------
 template <int D, int NG, bool K8 = false, int NGK = NG, bool V8 = false, bool K16 = false,
-          bool V16 = false>
+          bool V16 = false, bool FEW = false>
 struct CoopLayout {
   // fp16 K rows (512 bytes per token and kv head with fp16 V) take 4 kv heads
   // per block, so that 32-token tiles of K and V (64 KB) double-buffer in
   // LDS; packed rows take 8
   static constexpr int kHeads = K16 ? 4 : 8;
-  static constexpr int WPS = kHeads / 2;           // waves copying each sub-tile
+  // Waves that issue the tile copies: all of them, or with FEW (8 kv heads,
+  // the wide-group layout) waves 0-3 only, one per SIMD.  A CU runs two of
+  // the 8 waves per SIMD, and the second wave on a SIMD, which issues after
+  // the first, reaches the tile barrier last; with FEW it has no copies to
+  // issue.  In interleaved A/B runs that shortened the wide-group partials
+  // (config 4: 79.0 -> 75.6 us, config 5: 290.2 -> 280.4 us) but not the
+  // group-pair ones (config 2 unchanged, config 3: 110.9 -> 112.5 us, whose
+  // stream segments restart the copies more often), which keep all 8.
+  static constexpr int NCW = (FEW && !K16) ? 4 : kHeads;
+  static constexpr bool ALL = NCW == kHeads;       // every wave copies
+  static constexpr int WPS = NCW / 2;              // waves copying each sub-tile
   static constexpr int HBK = K16 ? 2 * D : K8 ? D : D / 2;   // K bytes per head and token
   static constexpr int HBV = V16 ? 2 * D : V8 ? D : D / 2;   // V bytes per head and token
   static constexpr int SBK = K16 ? 0 : 2 * NGK;    // K scale bytes per head and token
@@ -1159,6 +1169,9 @@ struct CoopLayout {
   static constexpr int NPWK = CPSK / WPS;          // code parts per wave and tile
   static constexpr int NPWV = CPSV / WPS;
   static constexpr int NJ = NPWK + NPWV;           // code copies per wave and tile
+  // scale arrays (K scales, V scales, K zeros, V zeros) per copying wave:
+  // four arrays of two sub-tiles over the copying waves
+  static constexpr int NSA = NCW == 4 && !K16 ? 2 : 1;
   static constexpr bool HAS_KZ = !K8 && !K16;      // K zero-points (asymmetric INT4 K)
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = K_OFF + 2 * 16 * CROWK;
@@ -1177,11 +1190,12 @@ struct CoopLayout {
   // a lane copies one 16-byte chunk of one scale row (the block's heads'
   // scales of one token), so rows must be whole chunks
   static_assert(SROWK % 16 == 0 && SROWV % 16 == 0, "scale rows of whole 16-byte chunks");
-  // The scale array wave w copies (of its sub-tile w % 2): 8 waves take
-  // array w / 2 (0 K scales, 1 V scales, 2 K zeros, 3 V zeros); with fp16 K
-  // (no K scales or zeros) 4 waves take V scales (w / 2 = 0) and V zeros.
-  __host__ __device__ static constexpr int s_array(int wave) {
-    return kHeads == 8 ? wave >> 1 : ((wave >> 1) == 0 ? 1 : 3);
+  // Scale array j of copying wave w (of its sub-tile w % 2): 8 waves take
+  // array w / 2 (0 K scales, 1 V scales, 2 K zeros, 3 V zeros), 4 copying
+  // waves of 8 arrays w / 2 and w / 2 + 2; with fp16 K (no K scales or
+  // zeros) 4 waves take V scales (w / 2 = 0) and V zeros.
+  __host__ __device__ static constexpr int s_array(int wave, int j = 0) {
+    return kHeads == 8 ? (wave >> 1) + 2 * j : ((wave >> 1) == 0 ? 1 : 3);
   }
   // scale array a: 0 K scales, 1 V scales, 2 K zeros, 3 V zeros
   __host__ __device__ static constexpr int s_off(int a) {
@@ -1206,20 +1220,28 @@ struct CoopLayout {
 
 // Loop-invariant addressing of the cooperative copy.  Strides are in bytes
 // and fit 32 bits (the host checks), so a page's address is one 32x32->64
-// multiply-add on the scalar unit.  Wave w copies sub-tile x = w % 2 only:
-// code parts w / 2 + 4k of K and V and the scale chunk of array w / 2, so
-// each wave looks up one page per tile.
+// multiply-add on the scalar unit.  Copying wave w copies sub-tile x = w % 2
+// only: code parts w / 2 + WPS k of K and V and the scale chunks of its
+// arrays (L::s_array), so each copying wave looks up one page per tile.
+struct CoopScale {
+  const uint8_t* sp;      // the scale array, head h0
+  uint32_t sp_b, sp_p;    // its block and page strides in bytes
+  uint32_t ls;            // this lane's byte offset in HBM
+  bool on;                // this wave copies it (wave-uniform)
+  bool lane_on;           // this lane copies a chunk
+  int lds;                // LDS offset of this wave's sub-tile of it
+};
+
 struct CoopAddr {
   const uint8_t* kc;      // codes of head h0 (block/page strides below)
   const uint8_t* vc;
-  const uint8_t* sp;      // this wave's scale array, head h0
-  uint32_t kc_b, kc_p, vc_b, vc_p, sp_b, sp_p;   // bytes
-  uint32_t lk[8], lv[8], ls;   // lane byte offsets in HBM (code parts, scale chunk)
+  uint32_t kc_b, kc_p, vc_b, vc_p;   // bytes
+  uint32_t lk[8], lv[8];  // lane byte offsets in HBM (code parts)
   bool same_kv;           // K and V codes share their strides (one page offset)
-  bool s_arr_on;          // this wave copies a scale array (wave-uniform)
-  bool s_on;              // this lane copies a scale chunk
+  bool copier;            // this wave issues copies (wave-uniform)
+  int nsc;                // scale copies per tile of this wave
   int x;                  // sub-tile this wave copies
-  int s_lds;              // LDS offset of this wave's scale sub-tile
+  CoopScale s0, s1;       // this wave's scale arrays (s1: four copying waves)
   const int32_t* bt;
   int bs_shift;
 };
@@ -1265,6 +1287,9 @@ __device__ __forceinline__ void lds_copy16(const void* base, uint32_t voff, cons
 template <class L>
 __device__ __forceinline__ void coop_issue(const CoopAddr& C, PageWindow& PW, int lane,
                                            int wave, int tb, int t_end, uint8_t* buf) {
+  if constexpr (!L::ALL) {
+    if (!C.copier) return;
+  }
   const int pb = (C.x == 0 || tb + 16 < t_end) ? tb + 16 * C.x : tb;
   const uint32_t pg = static_cast<uint32_t>(PW.page(C.bt, lane, pb >> C.bs_shift));
   const uint32_t of = static_cast<uint32_t>(pb & ((1 << C.bs_shift) - 1));
@@ -1278,10 +1303,14 @@ __device__ __forceinline__ void coop_issue(const CoopAddr& C, PageWindow& PW, in
   for (int k = 0; k < L::NPWK; ++k) lds_copy16(C.kc + ok, C.lk[k], dk + k * L::WPS * 1024);
 #pragma unroll
   for (int k = 0; k < L::NPWV; ++k) lds_copy16(C.vc + ov, C.lv[k], dv + k * L::WPS * 1024);
-  if (C.s_arr_on) {
-    const uint64_t os = static_cast<uint64_t>(pg) * C.sp_b + of * C.sp_p;
-    if (C.s_on) lds_copy16(C.sp + os, C.ls, buf + C.s_lds);
-  }
+  const auto scale_copy = [&](const CoopScale& S) {
+    if (S.on) {
+      const uint64_t os = static_cast<uint64_t>(pg) * S.sp_b + of * S.sp_p;
+      if (S.lane_on) lds_copy16(S.sp + os, S.ls, buf + S.lds);
+    }
+  };
+  scale_copy(C.s0);
+  if constexpr (L::NSA == 2) scale_copy(C.s1);
 }
 
 // s_waitcnt for "at most N vector-memory operations outstanding" (gfx9
@@ -1293,16 +1322,32 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Wait until this wave's copies of the next tile have landed, leaving the
-// copies of `later` further tiles in flight (each tile is NJ copies, plus one
-// for the waves that copy a scale array).
-template <int NJ>
-__device__ __forceinline__ void wait_tile_copies(int later, bool scale_wave) {
-  if (later <= 0) {
+// copies of `later` (<= 2) further tiles in flight: each tile is NJ code
+// copies and C.nsc scale copies of a copying wave.  A wave that copies
+// nothing has nothing to wait for (the block barrier after this orders its
+// reads behind the copying waves' waits).
+template <int PER>
+__device__ __forceinline__ void wait_later_tiles(int later) {
+  if (later <= 0)
     wait_vmcnt<0>();
-  } else if (later == 1) {
-    if (scale_wave) wait_vmcnt<NJ + 1>(); else wait_vmcnt<NJ>();
+  else if (later == 1)
+    wait_vmcnt<PER>();
+  else
+    wait_vmcnt<2 * PER>();
+}
+
+template <class L>
+__device__ __forceinline__ void wait_tile_copies(int later, const CoopAddr& C) {
+  if constexpr (L::NSA == 1) {
+    if (C.s0.on) wait_later_tiles<L::NJ + 1>(later); else wait_later_tiles<L::NJ>(later);
   } else {
-    if (scale_wave) wait_vmcnt<2 * (NJ + 1)>(); else wait_vmcnt<2 * NJ>();
+    if (!C.copier) return;
+    if (C.nsc == 0)
+      wait_later_tiles<L::NJ>(later);
+    else if (C.nsc == 1)
+      wait_later_tiles<L::NJ + 1>(later);
+    else
+      wait_later_tiles<L::NJ + 2>(later);
   }
 }
 
@@ -1469,7 +1514,7 @@ __device__ __forceinline__ void coop_tile(WS (&W)[NSET], const CoopAddr& C, int 
                                                           alo[s]);
   }
   // copies issued after tile i + 1's: tiles i + 2 .. min(i + NBUF - 1, ntiles - 1)
-  wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
+  wait_tile_copies<L>(min(NBUF - 2, ntiles - 2 - i), C);
   __syncthreads();
 }
 
@@ -2004,7 +2049,7 @@ __device__ __forceinline__ void coop_tile_w(WaveStateW<NGV, VASYM, K8, KASYM>& W
   const float svmax = W.template vscales<MASK>(st, valid, sv);
   if (W.slow_tile(score, svmax)) W.slow_step(score, svmax);
   W.template probs<MASK>(st, valid, score, sv, aw);
-  wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 2 - i), C.s_arr_on);
+  wait_tile_copies<L>(min(NBUF - 2, ntiles - 2 - i), C);
   __syncthreads();
 }
 
@@ -2025,7 +2070,7 @@ __device__ __forceinline__ void coop_segment(
                   [CoopLayout<D, NG, K8, NGK, V8, K16, V16>::BYTES],
     int seq, int hg, int t_begin, int seg_tokens, int seq_len_known, int64_t base0,
     int64_t stride) {
-  using L = CoopLayout<D, NG, K8, NGK, V8, K16, V16>;
+  using L = CoopLayout<D, NG, K8, NGK, V8, K16, V16, WIDE>;
   constexpr int NCH = D / 32;
   constexpr int KCH = K16 ? 4 * NCH : K8 ? 2 * NCH : NCH;
   constexpr int NBUF = L::NBUF;
@@ -2056,8 +2101,8 @@ __device__ __forceinline__ void coop_segment(
     C.vc_p = static_cast<uint32_t>(VEB * V.stride_page);
     C.same_kv = C.kc_b == C.vc_b && C.kc_p == C.vc_p;
     // code copy: lane -> LDS byte part*1024 + 16*lane of a sub-tile, which
-    // holds logical chunk (physical chunk) ^ row of that row; this wave's
-    // parts are (wave >> 1) + WPS k
+    // holds logical chunk (physical chunk) ^ row of that row; a copying
+    // wave's parts are (wave >> 1) + WPS k
 #pragma unroll
     for (int k = 0; k < L::NPWK; ++k) {
       const int byte = ((wave >> 1) + L::WPS * k) % L::CPSK * 1024 + 16 * lane;
@@ -2072,36 +2117,45 @@ __device__ __forceinline__ void coop_segment(
       const int c = ((byte % L::CROWV) >> 4) ^ r;
       C.lv[k] = static_cast<uint32_t>(r * C.vc_p + 16 * c);
     }
-    // wave w copies scale array L::s_array(w) (ks, vs, kz, vz) of sub-tile w % 2
-    const int arr = L::s_array(wave);
+    // copying wave w copies scale arrays L::s_array(w, j) (ks, vs, kz, vz)
+    // of sub-tile w % 2
+    C.copier = L::ALL || wave < L::NCW;
     C.x = wave & 1;
-    const uint16_t* base = arr == 0 ? static_cast<const uint16_t*>(K.scales)
-                         : arr == 1 ? static_cast<const uint16_t*>(V.scales)
-                         : arr == 2 ? static_cast<const uint16_t*>(K.zeros)
-                                    : static_cast<const uint16_t*>(V.zeros);
-    const int64_t sh = arr == 0 ? K.s_stride_head : arr == 1 ? V.s_stride_head
-                     : arr == 2 ? K.z_stride_head : V.z_stride_head;
-    const int64_t sbk = arr == 0 ? K.s_stride_block : arr == 1 ? V.s_stride_block
-                      : arr == 2 ? K.z_stride_block : V.z_stride_block;
-    const int64_t spg = arr == 0 ? K.s_stride_page : arr == 1 ? V.s_stride_page
-                      : arr == 2 ? K.z_stride_page : V.z_stride_page;
-    // (fp16 planes have no scales or zero-points)
-    const bool arr_on = (arr == 0 && !K16) || (arr == 1 && !V16) || (arr == 2 && KASYM) ||
-                        (arr == 3 && VASYM);
-    const int srow = L::s_row(arr);
-    C.s_arr_on = arr_on;
-    C.s_on = arr_on && lane < srow;
-    C.sp = arr_on ? reinterpret_cast<const uint8_t*>(base + h0 * sh) : nullptr;
-    C.sp_b = static_cast<uint32_t>(2 * sbk);
-    C.sp_p = static_cast<uint32_t>(2 * spg);
-    C.ls = 0;
-    if (arr_on) {
-      const int byte = 16 * lane;
-      const int r = byte / srow;
-      const int c = ((byte % srow) >> 4) ^ L::scale_swz(srow, r);
-      C.ls = static_cast<uint32_t>(r * C.sp_p + 16 * c);
+    const auto scale_addr = [&](CoopScale& S, int arr) {
+      const uint16_t* base = arr == 0 ? static_cast<const uint16_t*>(K.scales)
+                           : arr == 1 ? static_cast<const uint16_t*>(V.scales)
+                           : arr == 2 ? static_cast<const uint16_t*>(K.zeros)
+                                      : static_cast<const uint16_t*>(V.zeros);
+      const int64_t sh = arr == 0 ? K.s_stride_head : arr == 1 ? V.s_stride_head
+                       : arr == 2 ? K.z_stride_head : V.z_stride_head;
+      const int64_t sbk = arr == 0 ? K.s_stride_block : arr == 1 ? V.s_stride_block
+                        : arr == 2 ? K.z_stride_block : V.z_stride_block;
+      const int64_t spg = arr == 0 ? K.s_stride_page : arr == 1 ? V.s_stride_page
+                        : arr == 2 ? K.z_stride_page : V.z_stride_page;
+      // (fp16 planes have no scales or zero-points)
+      const bool arr_on = C.copier && ((arr == 0 && !K16) || (arr == 1 && !V16) ||
+                                       (arr == 2 && KASYM) || (arr == 3 && VASYM));
+      const int srow = L::s_row(arr);
+      S.on = arr_on;
+      S.lane_on = arr_on && lane < srow;
+      S.sp = arr_on ? reinterpret_cast<const uint8_t*>(base + h0 * sh) : nullptr;
+      S.sp_b = static_cast<uint32_t>(2 * sbk);
+      S.sp_p = static_cast<uint32_t>(2 * spg);
+      S.ls = 0;
+      if (arr_on) {
+        const int byte = 16 * lane;
+        const int r = byte / srow;
+        const int c = ((byte % srow) >> 4) ^ L::scale_swz(srow, r);
+        S.ls = static_cast<uint32_t>(r * S.sp_p + 16 * c);
+      }
+      S.lds = L::s_off(arr) + C.x * 16 * srow;
+    };
+    scale_addr(C.s0, L::s_array(wave, 0));
+    C.nsc = C.s0.on ? 1 : 0;
+    if constexpr (L::NSA == 2) {
+      scale_addr(C.s1, L::s_array(wave, 1));
+      C.nsc += C.s1.on ? 1 : 0;
     }
-    C.s_lds = L::s_off(arr) + C.x * 16 * srow;
     C.bt = a.block_table + seq * a.bt_stride;
     C.bs_shift = a.block_shift;
   }
@@ -2145,7 +2199,7 @@ __device__ __forceinline__ void coop_segment(
   if constexpr (WIDE) {
     WaveStateW<NG, VASYM, K8, KASYM> W;
     init_wave_w(W, qw[0], a, col, blk);
-    wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
+    wait_tile_copies<L>(min(NBUF - 2, ntiles - 1), C);
     __syncthreads();
     uint32_t vb[4][4];
     h8 aw[NG];
@@ -2173,7 +2227,7 @@ __device__ __forceinline__ void coop_segment(
   for (int s = 0; s < NSET; ++s)
     init_wave<D, NG, KASYM, VASYM, KCH, NGK, V8, V16>(W[s], qw[s], a, col, blk,
                                                       s * heads_per_set<NG>());
-  wait_tile_copies<L::NJ>(min(NBUF - 2, ntiles - 1), C.s_arr_on);
+  wait_tile_copies<L>(min(NBUF - 2, ntiles - 1), C);
   __syncthreads();
   // tile 0 (no PV pending), full tiles, an optional partial last tile, and
   // the PV of the last tile
