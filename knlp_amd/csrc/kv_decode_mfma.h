@@ -1145,14 +1145,15 @@ struct CoopLayout {
   // per block, so that 32-token tiles of K and V (64 KB) double-buffer in
   // LDS; packed rows take 8
   static constexpr int kHeads = K16 ? 4 : 8;
-  // Waves that issue the tile copies: all of them, or with FEW (8 kv heads,
-  // the wide-group layout) waves 0-3 only, one per SIMD.  A CU runs two of
-  // the 8 waves per SIMD, and the second wave on a SIMD, which issues after
-  // the first, reaches the tile barrier last; with FEW it has no copies to
-  // issue.  In interleaved A/B runs that shortened the wide-group partials
-  // (config 4: 79.0 -> 75.6 us, config 5: 290.2 -> 280.4 us) but not the
-  // group-pair ones (config 2 unchanged, config 3: 110.9 -> 112.5 us, whose
-  // stream segments restart the copies more often), which keep all 8.
+  // Waves that issue the tile copies: all of them, or with FEW (8 kv heads)
+  // waves 0-3 only, one per SIMD.  A CU runs two of the 8 waves per SIMD,
+  // and the second wave on a SIMD, which issues after the first, reaches the
+  // tile barrier last; with FEW it has no copies to issue.  In interleaved
+  // A/B runs that shortened the split-K partials (config 4: 79.0 -> 75.6 us,
+  // config 5: 290.2 -> 280.4, config 8: 96.6 -> 92.1, config 6: 51.6 ->
+  // 50.0) but lengthened the stream schedule's at config 3 (112.5 -> 113.5
+  // us, segments restarting the copies often): the stream kernel keeps all
+  // 8 except in the wide-group layout.
   static constexpr int NCW = (FEW && !K16) ? 4 : kHeads;
   static constexpr bool ALL = NCW == kHeads;       // every wave copies
   static constexpr int WPS = NCW / 2;              // waves copying each sub-tile
@@ -2061,16 +2062,17 @@ __device__ __forceinline__ void coop_tile_w(WaveStateW<NGV, VASYM, K8, KASYM>& W
 // empty.
 // WIDE: the wide-group wave state (WaveStateW: one set for 5 <= G <= 8,
 // INT8 K with one scale per row, INT4 V with NG groups, D = 128).  K16 / V16:
-// fp16 K (4 kv heads per block) / fp16 V.
+// fp16 K (4 kv heads per block) / fp16 V.  FEW: waves 0-3 issue every tile
+// copy (CoopLayout).
 template <int D, int NG, bool KASYM, bool VASYM, bool K8, int NGK, int NSET, bool V8,
-          bool WIDE = false, bool K16 = false, bool V16 = false>
+          bool WIDE = false, bool K16 = false, bool V16 = false, bool FEW = false>
 __device__ __forceinline__ void coop_segment(
     const DecodeArgs& a,
     uint8_t (&lds)[CoopLayout<D, NG, K8, NGK, V8, K16, V16>::NBUF]
                   [CoopLayout<D, NG, K8, NGK, V8, K16, V16>::BYTES],
     int seq, int hg, int t_begin, int seg_tokens, int seq_len_known, int64_t base0,
     int64_t stride) {
-  using L = CoopLayout<D, NG, K8, NGK, V8, K16, V16, WIDE>;
+  using L = CoopLayout<D, NG, K8, NGK, V8, K16, V16, FEW>;
   constexpr int NCH = D / 32;
   constexpr int KCH = K16 ? 4 * NCH : K8 ? 2 * NCH : NCH;
   constexpr int NBUF = L::NBUF;
@@ -2323,7 +2325,8 @@ __device__ __forceinline__ void coop_kernel_body(
     const int seq = blockIdx.y;
     const int hg = blockIdx.z;
     const int64_t row0 = static_cast<int64_t>(seq) * a.num_q_heads + (hg * L::kHeads + wave) * a.group;
-    coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16>(
+    // (four copying waves: shorter tile loops in every layout)
+    coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, true>(
         a, lds, seq, hg, split * a.split_tokens, a.split_tokens, -1,
         row0 * a.num_splits + split, a.num_splits);
   } else {
@@ -2391,7 +2394,10 @@ __device__ __forceinline__ void coop_kernel_body(
       KArgs* kp = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
       asm volatile("" : "+s"(kp));
       const DecodeArgs& A = *(const DecodeArgs*)kp;
-      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16>(
+      // (four copying waves for the wide-group layout only: a segment's
+      // start issues its first tiles' copies on those waves alone, and the
+      // stream schedule starts segments more often)
+      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, WIDE>(
           A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
           static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
       StreamWalk V = StreamWalk::uniform(walk);
