@@ -1582,23 +1582,38 @@ struct StreamStart {
   uint32_t n, cost;
   int s, len, Pe;
 
+  // The length scan below in chunks of 64 sequences: KN = 1 (up to 64
+  // sequences) or KMAX.  Its loops are unrolled over KN chunks, and each
+  // chunk's loads and scans run whether or not the chunk holds a sequence:
+  // at config 2 on the stream schedule one chunk takes the kernel from entry
+  // to its first segment in 2.0 us where sixteen took 3.7 (the partial 57.8
+  // -> 56.3 us, config 3's 109.3 -> 107.8 us).
   __device__ __forceinline__ void find(const DecodeArgs& a, int nhg, int b, int P, int lane,
                                        uint64_t* f0, uint64_t* f1) {
+    if (a.num_seqs <= kWave)
+      find_n<1>(a, nhg, b, P, lane, f0, f1);
+    else
+      find_n<KMAX>(a, nhg, b, P, lane, f0, f1);
+  }
+
+  template <int KN>
+  __device__ __forceinline__ void find_n(const DecodeArgs& a, int nhg, int b, int P, int lane,
+                                         uint64_t* f0, uint64_t* f1) {
     const int nk = (a.num_seqs + kWave - 1) / kWave;
-    int len_k[KMAX];
+    int len_k[KN];
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
+    for (int k = 0; k < KN; ++k) {
       const int i = kWave * k + lane;
       len_k[k] = (k < nk && i < a.num_seqs) ? a.seq_lens[i] : 0;
     }
     // all rows' tiles (nhg rows per sequence), and whether every non-empty
     // sequence has the same tile count (that of lane 0's first non-empty one)
-    uint32_t incl[KMAX];
+    uint32_t incl[KN];
     uint64_t tiles = 0;
     uint32_t nonempty = 0, tref = 0;
     bool ragged = false;
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
+    for (int k = 0; k < KN; ++k) {
       incl[k] = 0;
       if (k < nk) {                                           // uniform
         const uint32_t t = seq_tiles(len_k[k], a.max_context);
@@ -1633,7 +1648,7 @@ struct StreamStart {
     if (cost != 0) {
       total = 0;
 #pragma unroll
-      for (int k = 0; k < KMAX; ++k) {
+      for (int k = 0; k < KN; ++k) {
         if (k < nk) {
           const uint32_t t = seq_tiles(len_k[k], a.max_context);
           incl[k] = wave_incl_scan(t > 0 ? t + cost : 0u);
@@ -1653,7 +1668,7 @@ struct StreamStart {
     uint64_t acc = 0;
     int kstar = 0;
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
+    for (int k = 0; k < KN; ++k) {
       const uint64_t csum =
           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[k]), 63));
       if (k == kstar && k + 1 < nk && static_cast<uint64_t>(nhg) * (acc + csum) <= f) {
@@ -1664,7 +1679,7 @@ struct StreamStart {
     int lk = 0;
     uint32_t ik = 0;
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
+    for (int k = 0; k < KN; ++k) {
       if (k == kstar) {
         lk = len_k[k];
         ik = incl[k];
