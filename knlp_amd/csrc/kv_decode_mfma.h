@@ -1581,6 +1581,7 @@ struct StreamStart {
   uint64_t T, sbase;
   uint32_t n, cost;
   int s, len, Pe;
+  bool aligned;      // equal rows starting on share boundaries: one row per block
 
   // The length scan below in chunks of 64 sequences: KN = 1 (up to 64
   // sequences) or KMAX.  Its loops are unrolled over KN chunks, and each
@@ -1640,7 +1641,7 @@ struct StreamStart {
     const uint64_t T0 = static_cast<uint64_t>(nhg) * tiles;
     const uint32_t rows = static_cast<uint32_t>(nhg) * nonempty;
     const uint32_t Pe0 = static_cast<uint32_t>(min(static_cast<uint64_t>(P), T0));
-    const bool aligned = !ragged && rows > 0 && Pe0 % rows == 0;
+    aligned = !ragged && rows > 0 && Pe0 % rows == 0;
     cost = !aligned && T0 >= static_cast<uint64_t>(a.stream_row_cost + 1) * P
                ? static_cast<uint32_t>(a.stream_row_cost) : 0u;
     // inclusive prefix sums of the sequences' positions (tiles plus charges)
@@ -2349,6 +2350,7 @@ __device__ __forceinline__ void coop_kernel_body(
     uint32_t walk;                  // StreamWalk::hold(): the walk's state in one VGPR
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int b = blockIdx.x;
+    bool one_row;                   // an aligned batch: this block's tiles lie in one row
     {
       const int nhg = a.num_kv_heads / L::kHeads;
       if (b == 0 && threadIdx.x == 0) a.stream_hdr[0] = L::kHeads * a.group;
@@ -2356,6 +2358,7 @@ __device__ __forceinline__ void coop_kernel_body(
       uint64_t f0, f1;
       st.find(a, nhg, b, gridDim.x, lane, &f0, &f1);
       if (f0 >= f1) return;                                   // uniform: no tiles here
+      one_row = st.aligned;
       StreamWalk W;
       W.f = f0;
       W.fe = f1;
@@ -2409,12 +2412,19 @@ __device__ __forceinline__ void coop_kernel_body(
       KArgs* kp = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
       asm volatile("" : "+s"(kp));
       const DecodeArgs& A = *(const DecodeArgs*)kp;
-      // (four copying waves for the wide-group layout only: a segment's
-      // start issues its first tiles' copies on those waves alone, and the
-      // stream schedule starts segments more often)
-      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, WIDE>(
-          A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
-          static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
+      // Four copying waves (CoopLayout) when the batch is aligned (each
+      // block then runs one segment, as split-K does), and for the
+      // wide-group layout; eight otherwise: a segment's start issues its
+      // first tiles' copies on the copying waves alone, and ragged batches
+      // start segments more often (config 3: 112.5 -> 113.5 us with four)
+      if (one_row)
+        coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, true>(
+            A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
+            static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
+      else
+        coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, WIDE>(
+            A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
+            static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
       StreamWalk V = StreamWalk::uniform(walk);
       if (V.f >= V.fe) break;
       __syncthreads();    // the next segment's copies reuse the tile buffers
