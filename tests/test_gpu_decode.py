@@ -179,6 +179,13 @@ BF16_CASES = [
     ("perhead_hkv4", [900, 17], 16, 4, 128, 1, 1, 32, 32, 1.0),
     ("d64_g2", [500], 16, 8, 64, 1, 1, 32, 32, 1.0),
     ("kint8_two_sets", [1100, 3], 40, 8, 128, 2, 1, 128, 32, 1.0),
+    # the cooperative fp16-K loader (4 kv heads per block) and the wide-group
+    # layout (INT4 K and V in two groups; INT8 K per row with G = 5)
+    ("coop16_fp16_fp16", [900, 17], 32, 8, 128, 3, 3, 128, 128, 1.0),
+    ("coop16_kfp16_vint4_g64", [700, 5], 32, 8, 128, 3, 1, 128, 64, 1.0),
+    ("coop16_kfp16_vint8_g32", [600], 32, 8, 128, 3, 2, 128, 32, 1.0),
+    ("wide_int4_g64", [1300, 33], 32, 8, 128, 1, 1, 64, 64, 1.0),
+    ("wide_kint8_row_g5", [900, 40], 40, 8, 128, 2, 1, 128, 32, 1.0),
 ]
 
 
