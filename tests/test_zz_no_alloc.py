@@ -81,6 +81,17 @@ def test_noalloc_stream_schedule_twice():
         assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
 
 
+@pytest.mark.parametrize("fmt,gs", [(3, 128), (2, 128)], ids=["fp16_kv", "int8_kv"])
+def test_noalloc_other_planes_twice(fmt, gs):
+    # fp16 K and V (the cooperative fp16-K kernel) and INT8 K and V, split and
+    # stream, the second call smaller than the first
+    for i, (lens, split) in enumerate((([2500, 700, 1900], 512), ([640, 17], 0))):
+        print(f"noalloc fmt {fmt} call {i}: seq_lens={lens} split={split}", flush=True)
+        q, planes, bt, sl = _case(lens, 32, 8, 128, fmt, gs, 120 + 10 * fmt + i)
+        ref, out = _both(q, planes, bt, sl, 8, 128, fmt, gs, split)
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+
 def test_noalloc_on_a_side_stream():
     """The scratch is the copy on the stream's device, looked up through the
     stream (a non-null one here), and the call runs on that stream."""
