@@ -1153,7 +1153,7 @@ struct CoopLayout {
   // config 5: 290.2 -> 280.4, config 8: 96.6 -> 92.1, config 6: 51.6 ->
   // 50.0) but lengthened the stream schedule's at config 3 (112.5 -> 113.5
   // us, segments restarting the copies often): the stream kernel keeps all
-  // 8 except in the wide-group layout.
+  // 8 for batches that are not aligned, except in the wide-group layout.
   static constexpr int NCW = (FEW && !K16) ? 4 : kHeads;
   static constexpr bool ALL = NCW == kHeads;       // every wave copies
   static constexpr int WPS = NCW / 2;              // waves copying each sub-tile
