@@ -1151,9 +1151,9 @@ struct CoopLayout {
   // tile barrier last; with FEW it has no copies to issue.  In interleaved
   // A/B runs that shortened the split-K partials (config 4: 79.0 -> 75.6 us,
   // config 5: 290.2 -> 280.4, config 8: 96.6 -> 92.1, config 6: 51.6 ->
-  // 50.0) but lengthened the stream schedule's at config 3 (112.5 -> 113.5
-  // us, segments restarting the copies often): the stream kernel keeps all
-  // 8 for batches that are not aligned, except in the wide-group layout.
+  // 50.0) and the stream schedule's at config 8 (96.6 -> 93.1 us), with
+  // config 2 and the ragged config 3 unchanged within the spread; both
+  // cooperative kernels use it.
   static constexpr int NCW = (FEW && !K16) ? 4 : kHeads;
   static constexpr bool ALL = NCW == kHeads;       // every wave copies
   static constexpr int WPS = NCW / 2;              // waves copying each sub-tile
@@ -1581,7 +1581,6 @@ struct StreamStart {
   uint64_t T, sbase;
   uint32_t n, cost;
   int s, len, Pe;
-  bool aligned;      // equal rows starting on share boundaries: one row per block
 
   // The length scan below in chunks of 64 sequences: KN = 1 (up to 64
   // sequences) or KMAX.  Its loops are unrolled over KN chunks, and each
@@ -1641,7 +1640,7 @@ struct StreamStart {
     const uint64_t T0 = static_cast<uint64_t>(nhg) * tiles;
     const uint32_t rows = static_cast<uint32_t>(nhg) * nonempty;
     const uint32_t Pe0 = static_cast<uint32_t>(min(static_cast<uint64_t>(P), T0));
-    aligned = !ragged && rows > 0 && Pe0 % rows == 0;
+    const bool aligned = !ragged && rows > 0 && Pe0 % rows == 0;
     cost = !aligned && T0 >= static_cast<uint64_t>(a.stream_row_cost + 1) * P
                ? static_cast<uint32_t>(a.stream_row_cost) : 0u;
     // inclusive prefix sums of the sequences' positions (tiles plus charges)
@@ -2350,7 +2349,6 @@ __device__ __forceinline__ void coop_kernel_body(
     uint32_t walk;                  // StreamWalk::hold(): the walk's state in one VGPR
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int b = blockIdx.x;
-    bool one_row;                   // an aligned batch: this block's tiles lie in one row
     {
       const int nhg = a.num_kv_heads / L::kHeads;
       if (b == 0 && threadIdx.x == 0) a.stream_hdr[0] = L::kHeads * a.group;
@@ -2358,7 +2356,6 @@ __device__ __forceinline__ void coop_kernel_body(
       uint64_t f0, f1;
       st.find(a, nhg, b, gridDim.x, lane, &f0, &f1);
       if (f0 >= f1) return;                                   // uniform: no tiles here
-      one_row = st.aligned;
       StreamWalk W;
       W.f = f0;
       W.fe = f1;
@@ -2412,19 +2409,10 @@ __device__ __forceinline__ void coop_kernel_body(
       KArgs* kp = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
       asm volatile("" : "+s"(kp));
       const DecodeArgs& A = *(const DecodeArgs*)kp;
-      // Four copying waves (CoopLayout) when the batch is aligned (each
-      // block then runs one segment, as split-K does), and for the
-      // wide-group layout; eight otherwise: a segment's start issues its
-      // first tiles' copies on the copying waves alone, and ragged batches
-      // start segments more often (config 3: 112.5 -> 113.5 us with four)
-      if (one_row)
-        coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, true>(
-            A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
-            static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
-      else
-        coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, WIDE>(
-            A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
-            static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
+      // (four copying waves, as split-K)
+      coop_segment<D, NG, KASYM, VASYM, K8, NGK, NSET, V8, WIDE, K16, V16, true>(
+          A, lds, U.s, hg, 32 * t0, 32 * (t1 - t0), U.len,
+          static_cast<int64_t>(b + row) * HG + wave * A.group, 1);
       StreamWalk V = StreamWalk::uniform(walk);
       if (V.f >= V.fe) break;
       __syncthreads();    // the next segment's copies reuse the tile buffers
